@@ -1,0 +1,134 @@
+/* exl3c4.h -- the C-ABI of exl3c4, an MI355X (gfx950, CDNA4, wave64) kernel library for radiance-exl3's routed-expert
+ * hot path: the EXL3 trellis-coded mixture-of-experts ops moe_exl3_prep_gu, moe_exl3_gate_up, moe_exl3_down and
+ * moe_exl3_gate_up_down.
+ *
+ * Two layers are exported from libexl3c4.so, both plain C (no torch or HIP types in any signature; a stream is an
+ * opaque hipStream_t passed as void*):
+ *
+ *  1. THE OP ENTRY POINTS BELOW (exl3c4_*). Each replaces one entry of the reference device library's internal C-ABI
+ *     (kernels/exl3r4d/exl3r4d_dev.h:75-109: exl3r4d_launch_gemm, exl3r4d_launch_prep, the fused gate_up_down launch)
+ *     and carries the reference op contract (docs/OPS-exl3.md:84-191, include/exl3_abi.h:160-288) on plain pointers:
+ *     what the radiance engine would hand over in RadArgs (kernels/exl3r4d/launch.c:150-250) arrives here already
+ *     unpacked. Launches allocate nothing, synchronise nothing and read no environment (kernels/exl3r4d/launch.c:1-3);
+ *     scratch is the caller's, sized by exl3c4_scratch_bytes from the geometry alone.
+ *
+ *  2. THE RADIANCE KERNEL-PLUGIN EXPORTS (rad_plugin_abi_version, rad_plugin_info, rad_kernel_schema_count/_at,
+ *     rad_kernel_count/_at, rad_kernel_concurrent; include/rad_shim.h, radiance-exl3_amd/csrc/exl3c4_plugin.c), the
+ *     same symbols the gfx1201 library exports (kernels/exl3r4d/rows.c:527-550), whose rows' launch hooks unpack RadArgs
+ *     into the structs below.
+ *
+ * Return codes are radiance's (tests/ref/test_exl3ref.py:44, docs/STEP0.md row 1.72): 0 OK, negative refusals, always
+ * returned BEFORE anything is written.
+ *
+ * THE STORED FORM of a codes plane (exl3c4_relayout). The canonical plane (include/exl3_encoding.h:12-13: uK, element
+ * (i, j) = the K-bit symbol of W_hat[k = j][n = i], LSB-first rows) is re-laid once at load time into this library's
+ * wave64 record: for a weight [N rows, K cols], blocks (strip nb = 0..N/32-1, kstep ks = 0..K/64-1) in nb-major order,
+ * each block 64 segments of K u32 words, segment X (X = c + 16 g, c = 2 s + t) being stream words [sK, sK + K) of tile
+ * (tk = 4 ks + g, tn = 2 nb + t) -- exactly the words one lane of a wave decodes for one 16x16x32 MFMA step. A lossless
+ * permutation of the exllamav3 tile stream (common/exl3_layout.c:62-104); exl3c4_unrelayout inverts it.
+ */
+#ifndef EXL3C4_H
+#define EXL3C4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3C4_ABI_VERSION 1
+
+/* radiance status codes (names at kernels/exl3r4d/launch.c:5-14; values tests/ref/test_exl3ref.py:44). */
+enum {
+    EXL3C4_OK = 0,
+    EXL3C4_E_SHAPE = -1,
+    EXL3C4_E_DTYPE = -2,
+    EXL3C4_E_ALIGN = -3,
+    EXL3C4_E_STRIDE = -4,
+    EXL3C4_E_SCHEMA = -9,
+    EXL3C4_E_INVAL = -12,
+    EXL3C4_E_UNSUPPORTED = -18,
+    EXL3C4_E_SCRATCH = -20,
+    EXL3C4_E_DEVICE = -21,
+};
+
+/* The ops, numbered as include/exl3_abi.h:292 numbers them. */
+enum { EXL3C4_DOWN = 0, EXL3C4_GATE_UP = 1, EXL3C4_PREP_GU = 2, EXL3C4_GU_DN = 3 };
+/* Codebooks, numbered as common/exl3_decode.h:60 numbers them. */
+enum { EXL3C4_CB_3INST = 0, EXL3C4_CB_MCG = 1, EXL3C4_CB_MUL1 = 2 };
+/* Activation dtypes. */
+enum { EXL3C4_F16 = 0, EXL3C4_BF16 = 1 };
+
+/* One class of experts (include/exl3_abi.h:186-206, 298-304): a weight table per plane. A table is a device pointer
+ * array (its *_stride 0: entry j at ((void**)base)[j], the engine's form) or one stacked device buffer (entry j at base
+ * + j * stride bytes, a tool's form). Class c of an n_class op holds experts e % n_class == c at entry e / n_class.
+ *   codes   the STORED record (exl3c4_relayout) of the expert's [rows, cols] weight
+ *   suh     f16 [cols]; suh1 f16 [cols] (gate_up / prep_gu: the up half's input scales)
+ *   svh     f16 [rows]; dn_suh f16 [rows / 2] (gate_up h_rot = 1: DOWN's suh of the same expert) */
+typedef struct Exl3c4Class {
+    int32_t     rows, cols;
+    const void* codes;
+    const void* suh;
+    const void* suh1;
+    const void* svh;
+    const void* dn_suh;
+    int64_t     codes_stride, suh_stride, suh1_stride, svh_stride, dn_suh_stride;
+} Exl3c4Class;
+
+/* One launch of one op (docs/OPS-exl3.md "The ops"). Every pointer is device memory.
+ *   x        gate_up a_rot 0 / prep_gu / gate_up_down: token rows [x_rows, >= max cols], f16 or bf16;
+ *            gate_up a_rot 1: prep_gu's xr [T, >= 2 max cols] f16; down: h [T, >= max cols] f16
+ *   y        gate_up: h f16 [T, max rows / 2]; down / gate_up_down: y bf16 [T, max rows]; prep_gu: xr f16
+ *            [T, 2 max cols] (rows outside the runs and columns past 2 C left as they were)
+ *   gate_up_down: cls[] is gate_up's geometry (with dn_suh), dn[] down's codes and svh ([cols, rows / 2] a class). */
+typedef struct Exl3c4Op {
+    int32_t        op;
+    int32_t        bits, codebook;
+    int32_t        n_class;            /* 1, 2 (the two-class ops) or 4 (the _mod4 forms) */
+    int32_t        h_rot, a_rot;
+    int64_t        M, n_expert, top_k; /* M: the band's token count, sizes scratch (include/exl3_abi.h:155-157) */
+    Exl3c4Class    cls[4];
+    Exl3c4Class    dn[4];
+    const void*    x;
+    int32_t        x_dtype;
+    int64_t        x_rows, x_cols, x_pitch;   /* elements */
+    const int32_t* sorted_tok;                /* [>= T] */
+    const int32_t* expert_offset;             /* [n_expert + 1] */
+    void*          y;
+    int64_t        T, y_cols, y_pitch;        /* rows, width, pitch (elements) of the output */
+} Exl3c4Op;
+
+/* Bytes of scratch a launch of this op needs, from its parameters only (M * top_k rows at the band top, the classes'
+ * geometry): docs/STEP0.md:142-146, kernels/exl3r4d/launch.c:263-275. Negative: the refusal the launch would give. */
+int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
+
+/* Checks, then launches, one op on `stream` (kernels/exl3r4d/launch.c:525-612, 687-790, 833-855). Nothing is written
+ * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
+int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
+
+/* W_hat of one stored weight [rows, cols] as fp16 bits [rows][w_pitch] on the device -- the same decode the GEMMs run,
+ * exposed so it can be compared bit for bit with common/exl3_decode.c:193-221. bits 1..8 (K = 1 is decoder-only,
+ * include/exl3_encoding.h:45-48). */
+int exl3c4_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
+                   int64_t w_pitch, void* stream);
+
+/* ------------------------------------------------------------------ the stored form (host, load time) */
+/* Bytes of the stored record of a [rows, cols] weight at K bits: rows * cols * K / 8. */
+int64_t exl3c4_record_bytes(int64_t rows, int64_t cols, int32_t bits);
+/* Canonical uK plane (rows row_bytes apart; 0 = dense) -> stored record (kernels/exl3r4d/layout.c:269-330 is the
+ * reference's hook for the same step). rows % 32 == 0 and cols % 64 == 0, bits 1..8. */
+int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64_t cols, int32_t bits, void* record);
+/* Stored record -> canonical plane (kernels/exl3r4d/layout.c:332-360): the bits of each row's elements are written,
+ * the rest of the plane is left as it was. */
+int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes);
+
+/* Library identity: "gfx950" and the ABI version above. */
+const char* exl3c4_build_target(void);
+int         exl3c4_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,131 @@
+/* exl3c4_layout.c -- the stored form of a codes plane, both directions (host, load time).
+ *
+ * The canonical plane (include/exl3_encoding.h:12-13) keeps the K-bit symbol of W_hat[k = j][n = i] at element (i, j),
+ * each row a bit stream LSB first from bit j K (common/exl3_decode.c:148-168). A tile (tk, tn) of the weight is the
+ * MSB-first stream of its 256 symbols in trellis-position order, position p at tile (r, c) = pos_to_tile(p)
+ * (common/exl3_decode.c:71-121; common/exl3_layout.c:62-104 is the reference's codes <-> record walk). The stored form
+ * of this library cuts every tile's 8 K words into 8 segments of K words (positions 32 s .. 32 s + 31) and places them
+ * where the wave that decodes them loads them with one contiguous access (include/exl3c4.h, "THE STORED FORM"):
+ *
+ *   block (nb, ks) = strip nb of 32 columns x step ks of 64 k, at block index nb * (cols / 64) + ks, 64 K words;
+ *   segment X = c + 16 g of the block (c = 2 s + t) = words [s K, s K + K) of tile (tk = 4 ks + g, tn = 2 nb + t).
+ *
+ * A lossless permutation of the bits; unrelayout is its inverse. Checked both ways against the oracle's record and
+ * against the device decode (tests). */
+#include <stdint.h>
+#include <string.h>
+
+#include "exl3c4.h"
+
+static void tile_map(int tr[256], int tc[256]) {
+    for (int p = 0; p < 256; ++p) {
+        const int L = p >> 3, j = p & 7;
+        tr[p] = 2 * (L & 3) + ((j & 1) | ((j & 2) << 2));
+        tc[p] = (L >> 2) + 8 * (j >> 2);
+    }
+}
+
+/* Tile (tk, tn)'s 8 K stream words from the plane: its 16 rows' 2 K bytes each, symbols LSB first, then the stream. */
+static void tile_words(const uint8_t* codes, int64_t rb, int64_t tk, int64_t tn, int bits, const int* tr,
+                       const int* tc, uint32_t* w) {
+    uint8_t sym[16][16];   /* [c][r]: row n = 16 tn + c, column k = 16 tk + r */
+    const uint32_t mask = (1u << bits) - 1u;
+    const int seg = 2 * bits;
+    for (int c = 0; c < 16; ++c) {
+        uint8_t b[18] = { 0 };
+        memcpy(b, codes + (tn * 16 + c) * rb + tk * seg, (size_t)seg);
+        for (int r = 0; r < 16; ++r) {
+            const int o = r * bits;
+            sym[c][r] = (uint8_t)((((uint32_t)b[o >> 3] | ((uint32_t)b[(o >> 3) + 1] << 8)) >> (o & 7)) & mask);
+        }
+    }
+    uint64_t acc = 0;
+    int nb = 0;
+    for (int p = 0; p < 256; ++p) {
+        acc = (acc << bits) | sym[tc[p]][tr[p]];
+        nb += bits;
+        if (nb >= 32) {
+            nb -= 32;
+            *w++ = (uint32_t)(acc >> nb);
+            acc &= (nb ? ((1ull << nb) - 1ull) : 0ull);
+        }
+    }
+}
+
+static void words_tile(const uint32_t* w, int64_t tk, int64_t tn, int bits, const int* tr, const int* tc,
+                       uint8_t* codes, int64_t rb) {
+    uint8_t sym[16][16];
+    const uint32_t mask = (1u << bits) - 1u;
+    uint64_t acc = 0;
+    int nb = 0;
+    for (int p = 0; p < 256; ++p) {
+        if (nb < bits) {
+            acc = (acc << 32) | *w++;
+            nb += 32;
+        }
+        nb -= bits;
+        sym[tc[p]][tr[p]] = (uint8_t)((acc >> nb) & mask);
+        acc &= (nb ? ((1ull << nb) - 1ull) : 0ull);
+    }
+    const int seg = 2 * bits;
+    for (int c = 0; c < 16; ++c) {
+        uint8_t b[18] = { 0 };
+        for (int r = 0; r < 16; ++r) {
+            const int o = r * bits;
+            const uint32_t v = (uint32_t)sym[c][r] << (o & 7);
+            b[o >> 3] |= (uint8_t)v;
+            b[(o >> 3) + 1] |= (uint8_t)(v >> 8);
+        }
+        memcpy(codes + (tn * 16 + c) * rb + tk * seg, b, (size_t)seg);
+    }
+}
+
+int64_t exl3c4_record_bytes(int64_t rows, int64_t cols, int32_t bits) { return rows * cols * bits / 8; }
+
+static int shape_ok(int64_t rows, int64_t cols, int bits) {
+    return bits >= 1 && bits <= 8 && rows > 0 && cols > 0 && rows % 32 == 0 && cols % 64 == 0;
+}
+
+/* Word offset of segment s of tile (tk, tn) in the stored record. */
+static int64_t seg_at(int64_t tk, int64_t tn, int s, int64_t ksteps, int bits) {
+    const int64_t nb = tn >> 1, ks = tk >> 2;
+    const int t = (int)(tn & 1), g = (int)(tk & 3);
+    const int X = (2 * s + t) + 16 * g;
+    return ((nb * ksteps + ks) * 64 + X) * bits;
+}
+
+int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64_t cols, int32_t bits, void* record) {
+    int tr[256], tc[256];
+    uint32_t w[64];
+    if (!codes || !record) return EXL3C4_E_INVAL;
+    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
+    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
+    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
+    tile_map(tr, tc);
+    uint32_t* out = (uint32_t*)record;
+    const int64_t ksteps = cols / 64;
+    for (int64_t tn = 0; tn < rows / 16; ++tn)
+        for (int64_t tk = 0; tk < cols / 16; ++tk) {
+            tile_words(codes, row_bytes, tk, tn, bits, tr, tc, w);
+            for (int s = 0; s < 8; ++s) memcpy(out + seg_at(tk, tn, s, ksteps, bits), w + s * bits, (size_t)bits * 4);
+        }
+    return EXL3C4_OK;
+}
+
+int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes) {
+    int tr[256], tc[256];
+    uint32_t w[64];
+    if (!codes || !record) return EXL3C4_E_INVAL;
+    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
+    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
+    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
+    tile_map(tr, tc);
+    const uint32_t* in = (const uint32_t*)record;
+    const int64_t ksteps = cols / 64;
+    for (int64_t tn = 0; tn < rows / 16; ++tn)
+        for (int64_t tk = 0; tk < cols / 16; ++tk) {
+            for (int s = 0; s < 8; ++s) memcpy(w + s * bits, in + seg_at(tk, tn, s, ksteps, bits), (size_t)bits * 4);
+            words_tile(w, tk, tn, bits, tr, tc, codes, row_bytes);
+        }
+    return EXL3C4_OK;
+}

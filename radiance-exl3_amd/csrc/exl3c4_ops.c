@@ -1,0 +1,298 @@
+/* exl3c4_ops.c -- the op entry points of include/exl3c4.h: refusals, scratch carving, and the launch sequence of each
+ * op on the caller's stream. Plain C over the device C-ABI (exl3c4_dev.h). Nothing here allocates, synchronises or
+ * reads the environment (the reference adapter's rule, kernels/exl3r4d/launch.c:1-3).
+ *
+ * WHAT A LAUNCH REFUSES, before anything is written (docs/OPS-exl3.md:292-301; kernels/exl3r4d/launch.c:5-14):
+ *   EXL3C4_E_INVAL    an unknown op, a required operand absent, h_rot / a_rot not 0 or 1, n_class not 1, 2 or 4,
+ *                     gate_up h_rot = 1 (or gate_up_down) without a class's dn_suh table
+ *   EXL3C4_E_DTYPE    K outside 2..8, an unknown codebook, an activation of a dtype the op does not read
+ *   EXL3C4_E_SHAPE    extents the format cannot hold (every K % 128, gate_up N % 256, down N % 128), a
+ *                     non-positive count, an output not exactly the op's width, an input narrower than it reads
+ *   EXL3C4_E_STRIDE   a row pitch below its width
+ *   EXL3C4_E_ALIGN    a sorted-row input the 16-byte activation loads cannot take; a misaligned table
+ *   EXL3C4_E_SCRATCH  less scratch than exl3c4_scratch_bytes asks for
+ * The routing VALUES live in device memory and are not read here (that would be a synchronisation): the kernels
+ * clamp every run to [0, T), so a malformed table gives wrong rows, never a stray write (launch.c:14-15). */
+#include <stdint.h>
+#include <string.h>
+
+#include "exl3c4.h"
+#include "exl3c4_dev.h"
+
+#define ALIGN_UP(x, a) (((x) + (a) - 1) / (a) * (a))
+
+static int is_gate_up(int op) { return op == EXL3C4_GATE_UP || op == EXL3C4_PREP_GU || op == EXL3C4_GU_DN; }
+
+static int64_t max_cols(const Exl3c4Op* o) {
+    int64_t m = 0;
+    for (int c = 0; c < o->n_class; ++c) m = o->cls[c].cols > m ? o->cls[c].cols : m;
+    return m;
+}
+static int64_t max_rows(const Exl3c4Op* o) {
+    int64_t m = 0;
+    for (int c = 0; c < o->n_class; ++c) m = o->cls[c].rows > m ? o->cls[c].rows : m;
+    return m;
+}
+
+/* Chunks of at most 16 rows the runs of T sorted rows can make over n_expert experts. */
+static int64_t chunk_bound(int64_t T, int64_t n_expert) {
+    return T / EXL3C4_CHUNK_ROWS + (n_expert < T ? n_expert : T) + 1;
+}
+
+/* Split-K of one GEMV launch, from the geometry alone (never the routing, so a row's bits do not depend on the batch):
+ * enough waves to fill the device, at most 16 splits and never more than the k steps. */
+static int ksplit_for(int64_t chunks, int64_t strips, int64_t ksteps) {
+    const int64_t units = chunks * strips;
+    int64_t s = units > 0 ? (8192 + units - 1) / units : 1;
+    if (s > 16) s = 16;
+    if (s > ksteps) s = ksteps;
+    return s < 1 ? 1 : (int)s;
+}
+
+typedef struct Carve {
+    int64_t plan, xr, part, h, total;
+    int64_t chunks, T, xr_pitch, part_pitch, h_pitch;
+    int     split_gu, split_dn;
+} Carve;
+
+/* The scratch of one launch with T sorted rows: [plan | xr | partials | h], each 256-B aligned. */
+static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
+    const int op = o->op;
+    const int64_t xc = max_cols(o), rc = max_rows(o);
+    memset(k, 0, sizeof *k);
+    k->T = T;
+    k->chunks = chunk_bound(T, o->n_expert);
+    int64_t off = 0;
+    k->plan = off;
+    off += ALIGN_UP(16 + 16 * k->chunks, 256);
+    k->xr = off;
+    if (op == EXL3C4_GATE_UP && !o->a_rot) k->xr_pitch = 2 * xc;
+    else if (op == EXL3C4_GU_DN) k->xr_pitch = 2 * xc;
+    else if (op == EXL3C4_DOWN && !o->h_rot) k->xr_pitch = xc;
+    off += ALIGN_UP(T * k->xr_pitch * 2, 256);
+    k->part = off;
+    int64_t part_cols = 0, part_splits = 1;
+    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
+        int64_t kmin = INT64_MAX;
+        for (int c = 0; c < o->n_class; ++c)
+            if (o->cls[c].cols / EXL3C4_KSTEP < kmin) kmin = o->cls[c].cols / EXL3C4_KSTEP;
+        k->split_gu = ksplit_for(k->chunks, rc / EXL3C4_STRIP, kmin);
+        if (rc > part_cols) part_cols = rc;
+        if (k->split_gu > part_splits) part_splits = k->split_gu;
+    }
+    if (op == EXL3C4_DOWN || op == EXL3C4_GU_DN) {
+        /* down's geometry: its own classes, or gate_up_down's [cols, rows / 2] */
+        int64_t kmin = INT64_MAX, nmax = 0;
+        for (int c = 0; c < o->n_class; ++c) {
+            const int64_t r = op == EXL3C4_DOWN ? o->cls[c].rows : o->cls[c].cols;
+            const int64_t kk = op == EXL3C4_DOWN ? o->cls[c].cols : o->cls[c].rows / 2;
+            if (kk / EXL3C4_KSTEP < kmin) kmin = kk / EXL3C4_KSTEP;
+            if (r > nmax) nmax = r;
+        }
+        k->split_dn = ksplit_for(k->chunks, nmax / EXL3C4_STRIP, kmin);
+        if (nmax > part_cols) part_cols = nmax;
+        if (k->split_dn > part_splits) part_splits = k->split_dn;
+    }
+    k->part_pitch = part_cols;
+    off += ALIGN_UP(part_splits * T * part_cols * 4, 256);
+    k->h = off;
+    if (op == EXL3C4_GU_DN) {
+        k->h_pitch = rc / 2;
+        off += ALIGN_UP(T * k->h_pitch * 2, 256);
+    }
+    k->total = off;
+}
+
+/* ------------------------------------------------------------------ refusals */
+
+static int class_ok(const Exl3c4Op* o, const Exl3c4Class* c, int gate_up_geom, int need_suh1, int need_dn_suh,
+                    int need_codes) {
+    if (c->cols <= 0 || c->cols % 128) return EXL3C4_E_SHAPE;
+    if (o->op != EXL3C4_PREP_GU && (c->rows <= 0 || c->rows % (gate_up_geom ? 256 : 128))) return EXL3C4_E_SHAPE;
+    if (!c->suh || (need_suh1 && !c->suh1) || (need_dn_suh && !c->dn_suh)) return EXL3C4_E_INVAL;
+    if (need_codes && (!c->codes || !c->svh)) return EXL3C4_E_INVAL;
+    if (c->codes_stride < 0 || c->suh_stride < 0 || c->suh1_stride < 0 || c->svh_stride < 0 || c->dn_suh_stride < 0)
+        return EXL3C4_E_STRIDE;
+    if (need_codes && c->codes_stride && (c->codes_stride % 4 || (uintptr_t)c->codes % 4)) return EXL3C4_E_ALIGN;
+    if ((c->suh_stride | c->suh1_stride | c->svh_stride | c->dn_suh_stride) & 1) return EXL3C4_E_ALIGN;
+    if (need_codes && c->codes_stride && c->codes_stride < exl3c4_record_bytes(c->rows, c->cols, o->bits))
+        return EXL3C4_E_STRIDE;
+    return EXL3C4_OK;
+}
+
+static int check(const Exl3c4Op* o) {
+    const int op = o->op;
+    if (op < EXL3C4_DOWN || op > EXL3C4_GU_DN) return EXL3C4_E_INVAL;
+    if (!o->x || !o->y || !o->sorted_tok || !o->expert_offset) return EXL3C4_E_INVAL;
+    if (o->n_class != 1 && o->n_class != 2 && o->n_class != 4) return EXL3C4_E_INVAL;
+    if ((o->h_rot != 0 && o->h_rot != 1) || (o->a_rot != 0 && o->a_rot != 1)) return EXL3C4_E_INVAL;
+    if (op != EXL3C4_GATE_UP && o->a_rot) return EXL3C4_E_INVAL;
+    if (o->bits < 2 || o->bits > 8) return EXL3C4_E_DTYPE;
+    if (op != EXL3C4_PREP_GU && (o->codebook < EXL3C4_CB_3INST || o->codebook > EXL3C4_CB_MUL1)) return EXL3C4_E_DTYPE;
+    if (o->M < 1 || o->n_expert < 1 || o->top_k < 1 || o->T < 0) return EXL3C4_E_SHAPE;
+    if (o->n_expert > 65536) return EXL3C4_E_SHAPE;
+    const int gu = is_gate_up(op);
+    for (int c = 0; c < o->n_class; ++c) {
+        const int need_dn = (op == EXL3C4_GATE_UP && o->h_rot) || op == EXL3C4_GU_DN;
+        const int rc = class_ok(o, &o->cls[c], gu, gu, need_dn, op != EXL3C4_PREP_GU);
+        if (rc) return rc;
+        if (op == EXL3C4_GU_DN) {
+            const Exl3c4Class* d = &o->dn[c];
+            if (!d->codes || !d->svh) return EXL3C4_E_INVAL;
+            if (d->rows != o->cls[c].cols || d->cols != o->cls[c].rows / 2) return EXL3C4_E_SHAPE;
+            if (d->codes_stride < 0 || d->svh_stride < 0) return EXL3C4_E_STRIDE;
+            if (d->codes_stride && (d->codes_stride % 4 || (uintptr_t)d->codes % 4)) return EXL3C4_E_ALIGN;
+            if (d->svh_stride & 1) return EXL3C4_E_ALIGN;
+        }
+    }
+    /* the input: token rows (f16 or bf16) or sorted rows (f16) */
+    const int token_rows = (op == EXL3C4_GATE_UP && !o->a_rot) || op == EXL3C4_PREP_GU || op == EXL3C4_GU_DN;
+    if (o->x_dtype != EXL3C4_F16 && !(token_rows && o->x_dtype == EXL3C4_BF16)) return EXL3C4_E_DTYPE;
+    const int64_t xc = max_cols(o), rc = max_rows(o);
+    const int64_t need_x = op == EXL3C4_GATE_UP && o->a_rot ? 2 * xc : xc;
+    if (o->x_cols < need_x) return EXL3C4_E_SHAPE;
+    if (o->x_pitch < o->x_cols) return EXL3C4_E_STRIDE;
+    if (!token_rows && o->x_rows < o->T) return EXL3C4_E_SHAPE;
+    if (token_rows && o->x_rows < 1 && o->T > 0) return EXL3C4_E_SHAPE;
+    const int gemm_reads_x = (op == EXL3C4_GATE_UP && o->a_rot) || (op == EXL3C4_DOWN && o->h_rot);
+    if (gemm_reads_x && ((uintptr_t)o->x % 16 || (o->x_pitch * 2) % 16)) return EXL3C4_E_ALIGN;
+    if ((uintptr_t)o->x % 2) return EXL3C4_E_ALIGN;
+    /* the output: exactly the op's width */
+    const int64_t want = op == EXL3C4_PREP_GU ? 2 * xc : op == EXL3C4_GATE_UP ? rc / 2 : op == EXL3C4_GU_DN ? xc : rc;
+    if (o->y_cols != want) return EXL3C4_E_SHAPE;
+    if (o->y_pitch < o->y_cols) return EXL3C4_E_STRIDE;
+    if ((uintptr_t)o->y % 2) return EXL3C4_E_ALIGN;
+    return EXL3C4_OK;
+}
+
+int64_t exl3c4_scratch_bytes(const Exl3c4Op* o) {
+    Exl3c4Op q;
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    q = *o;
+    q.T = o->M * o->top_k;
+    if ((rc = check(&q)) != EXL3C4_OK) return rc;
+    Carve k;
+    carve(&q, q.T > o->T ? q.T : o->T, &k);
+    return k.total;
+}
+
+/* ------------------------------------------------------------------ the launch */
+
+static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* a) {
+    memset(a, 0, sizeof *a);
+    a->sorted = o->sorted_tok;
+    a->off = o->expert_offset;
+    a->plan = (int32_t*)(s + k->plan);
+    a->part = (float*)(s + k->part);
+    a->part_pitch = k->part_pitch;
+    a->part_split = k->T * k->part_pitch;
+    a->T = (int32_t)o->T;
+    a->n_expert = (int32_t)o->n_expert;
+    a->top_k = (int32_t)o->top_k;
+    a->n_class = o->n_class;
+    a->max_chunks = (int32_t)k->chunks;
+    a->bits = o->bits;
+    a->codebook = o->codebook;
+    a->x_dtype = o->x_dtype;
+    a->x_rows = (int32_t)o->x_rows;
+}
+
+int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    Carve k;
+    carve(o, o->T, &k);
+    if (k.total > 0 && (!scratch || scratch_bytes < k.total || (uintptr_t)scratch % 256)) return EXL3C4_E_SCRATCH;
+    if (o->T == 0) return EXL3C4_OK;
+    char* s = (char*)scratch;
+    const int op = o->op;
+    const int64_t xc = max_cols(o), rcw = max_rows(o);
+    Exl3c4Launch a;
+    base_args(o, &k, s, &a);
+    for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
+
+    if (op == EXL3C4_PREP_GU) {
+        a.x = o->x; a.x_pitch = o->x_pitch;
+        a.y = o->y; a.y_pitch = o->y_pitch;
+        a.prep_mode = EXL3C4_PREP_GU_OP;
+        return exl3c4_dev_prep(&a, 2, stream);
+    }
+    if ((rc = exl3c4_dev_plan(&a, stream)) != 0) return rc;
+
+    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
+        if (op == EXL3C4_GU_DN || !o->a_rot) {
+            a.x = o->x; a.x_pitch = o->x_pitch;
+            a.y = s + k.xr; a.y_pitch = k.xr_pitch;
+            a.prep_mode = EXL3C4_PREP_GU_SCRATCH;
+            if ((rc = exl3c4_dev_prep(&a, 2, stream)) != 0) return rc;
+            a.a = s + k.xr; a.a_pitch = k.xr_pitch;
+        } else {
+            a.a = o->x; a.a_pitch = o->x_pitch;
+        }
+        a.gate_up = 1;
+        a.ksplit = k.split_gu;
+        a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
+        if ((rc = exl3c4_dev_gemv(&a, stream)) != 0) return rc;
+        if (op == EXL3C4_GATE_UP) {
+            a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
+            a.h_rot = o->h_rot;
+            return exl3c4_dev_epilogue(&a, stream);
+        }
+        a.y = s + k.h; a.y_pitch = k.h_pitch; a.y_cols = (int32_t)k.h_pitch;
+        a.h_rot = 1;
+        if ((rc = exl3c4_dev_epilogue(&a, stream)) != 0) return rc;
+        /* down over h: gate_up_down's down classes [cols, rows / 2], suh = gate_up's dn_suh (include/exl3_abi.h:
+         * 751-800); h crosses rotated (h_rot = 1) */
+        Exl3c4Launch d;
+        base_args(o, &k, s, &d);
+        int64_t nmax = 0;
+        for (int c = 0; c < o->n_class; ++c) {
+            d.cls[c] = o->dn[c];
+            d.cls[c].rows = o->cls[c].cols;
+            d.cls[c].cols = o->cls[c].rows / 2;
+            d.cls[c].suh = o->cls[c].dn_suh;
+            d.cls[c].suh_stride = o->cls[c].dn_suh_stride;
+            if (d.cls[c].rows > nmax) nmax = d.cls[c].rows;
+        }
+        d.a = s + k.h; d.a_pitch = k.h_pitch;
+        d.gate_up = 0;
+        d.ksplit = k.split_dn;
+        d.max_strips = (int32_t)(nmax / EXL3C4_STRIP);
+        if ((rc = exl3c4_dev_gemv(&d, stream)) != 0) return rc;
+        d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
+        return exl3c4_dev_epilogue(&d, stream);
+    }
+
+    /* down */
+    if (!o->h_rot) {
+        a.x = o->x; a.x_pitch = o->x_pitch;
+        a.y = s + k.xr; a.y_pitch = k.xr_pitch;
+        a.prep_mode = EXL3C4_PREP_DN;
+        if ((rc = exl3c4_dev_prep(&a, 1, stream)) != 0) return rc;
+        a.a = s + k.xr; a.a_pitch = k.xr_pitch;
+    } else {
+        a.a = o->x; a.a_pitch = o->x_pitch;
+    }
+    (void)xc;
+    a.gate_up = 0;
+    a.ksplit = k.split_dn;
+    a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
+    if ((rc = exl3c4_dev_gemv(&a, stream)) != 0) return rc;
+    a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
+    return exl3c4_dev_epilogue(&a, stream);
+}
+
+int exl3c4_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
+                   int64_t w_pitch, void* stream) {
+    if (!record || !w_hat) return EXL3C4_E_INVAL;
+    if (bits < 1 || bits > 8 || codebook < EXL3C4_CB_3INST || codebook > EXL3C4_CB_MUL1) return EXL3C4_E_DTYPE;
+    if (rows <= 0 || cols <= 0 || rows % EXL3C4_STRIP || cols % EXL3C4_KSTEP) return EXL3C4_E_SHAPE;
+    if (w_pitch < cols) return EXL3C4_E_STRIDE;
+    if ((uintptr_t)record % 4 || (uintptr_t)w_hat % 2) return EXL3C4_E_ALIGN;
+    return exl3c4_dev_dequant(record, rows, cols, bits, codebook, w_hat, w_pitch, stream);
+}
+
+const char* exl3c4_build_target(void) { return "gfx950"; }
+int         exl3c4_abi_version(void) { return EXL3C4_ABI_VERSION; }

@@ -1,0 +1,161 @@
+"""exl3c4.py -- Python binding of libexl3c4.so (include/exl3c4.h) for tests and the benchmark.
+
+The library is C over HIP; this module only marshals pointers. torch is used for device memory and the stream
+(plumbing), never for the computation: every op runs in the library's HIP kernels. If libexl3c4.so is missing this
+module raises -- there is no fallback of any kind.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libexl3c4.so")
+
+DOWN, GATE_UP, PREP_GU, GU_DN = 0, 1, 2, 3
+CB = {"3inst": 0, "mcg": 1, "mul1": 2}
+F16, BF16 = 0, 1
+STATUS = {0: "OK", -1: "RAD_E_SHAPE", -2: "RAD_E_DTYPE", -3: "RAD_E_ALIGN", -4: "RAD_E_STRIDE", -9: "RAD_E_SCHEMA",
+          -12: "RAD_E_INVAL", -18: "RAD_E_UNSUPPORTED", -20: "RAD_E_SCRATCH", -21: "RAD_E_DEVICE"}
+
+_lib = None
+_p = C.c_void_p
+_i64 = C.c_int64
+_i32 = C.c_int32
+
+
+class Class(C.Structure):
+    _fields_ = [("rows", _i32), ("cols", _i32),
+                ("codes", _p), ("suh", _p), ("suh1", _p), ("svh", _p), ("dn_suh", _p),
+                ("codes_stride", _i64), ("suh_stride", _i64), ("suh1_stride", _i64), ("svh_stride", _i64),
+                ("dn_suh_stride", _i64)]
+
+
+class Op(C.Structure):
+    _fields_ = [("op", _i32), ("bits", _i32), ("codebook", _i32), ("n_class", _i32), ("h_rot", _i32), ("a_rot", _i32),
+                ("M", _i64), ("n_expert", _i64), ("top_k", _i64),
+                ("cls", Class * 4), ("dn", Class * 4),
+                ("x", _p), ("x_dtype", _i32), ("x_rows", _i64), ("x_cols", _i64), ("x_pitch", _i64),
+                ("sorted_tok", _p), ("expert_offset", _p),
+                ("y", _p), ("T", _i64), ("y_cols", _i64), ("y_pitch", _i64)]
+
+
+def lib():
+    """The loaded library; raises when it has not been built (no CPU or torch fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        L = C.CDLL(LIB_PATH)
+        L.exl3c4_scratch_bytes.restype = _i64
+        L.exl3c4_scratch_bytes.argtypes = [C.POINTER(Op)]
+        L.exl3c4_launch.restype = C.c_int
+        L.exl3c4_launch.argtypes = [C.POINTER(Op), _p, _i64, _p]
+        L.exl3c4_dequant.restype = C.c_int
+        L.exl3c4_dequant.argtypes = [_p, _i32, _i32, _i32, _i32, _p, _i64, _p]
+        L.exl3c4_record_bytes.restype = _i64
+        L.exl3c4_record_bytes.argtypes = [_i64, _i64, _i32]
+        L.exl3c4_relayout.restype = C.c_int
+        L.exl3c4_relayout.argtypes = [_p, _i64, _i64, _i64, _i32, _p]
+        L.exl3c4_unrelayout.restype = C.c_int
+        L.exl3c4_unrelayout.argtypes = [_p, _i64, _i64, _i32, _p, _i64]
+        L.exl3c4_build_target.restype = C.c_char_p
+        L.exl3c4_abi_version.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+# ------------------------------------------------------------------------------------------ stored form (host)
+def relayout(codes: np.ndarray, rows: int, cols: int, bits: int) -> np.ndarray:
+    """Canonical uK plane [rows][row_bytes] -> the stored record (uint8 [rows*cols*bits/8])."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.zeros(rows * cols * bits // 8, np.uint8)
+    rc = lib().exl3c4_relayout(codes.ctypes.data, codes.shape[-1], rows, cols, bits, out.ctypes.data)
+    if rc:
+        raise ValueError(f"exl3c4_relayout: {STATUS.get(rc, rc)}")
+    return out
+
+
+def unrelayout(record: np.ndarray, rows: int, cols: int, bits: int) -> np.ndarray:
+    record = np.ascontiguousarray(record, dtype=np.uint8)
+    rb = (cols * bits + 7) // 8
+    out = np.zeros((rows, rb), np.uint8)
+    rc = lib().exl3c4_unrelayout(record.ctypes.data, rows, cols, bits, out.ctypes.data, rb)
+    if rc:
+        raise ValueError(f"exl3c4_unrelayout: {STATUS.get(rc, rc)}")
+    return out
+
+
+# ------------------------------------------------------------------------------------------ device calls
+def _stream(stream):
+    import torch
+    s = torch.cuda.current_stream() if stream is None else stream
+    return C.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def dequant(record, rows: int, cols: int, bits: int, cb, stream=None):
+    """W_hat fp16 bits (torch.int16 [rows, cols]) of a stored record on the device."""
+    import torch
+    out = torch.empty((rows, cols), dtype=torch.int16, device=record.device)
+    rc = lib().exl3c4_dequant(_ptr(record), rows, cols, bits, CB.get(cb, cb), _ptr(out), cols, _stream(stream))
+    if rc:
+        raise RuntimeError(f"exl3c4_dequant: {STATUS.get(rc, rc)}")
+    return out
+
+
+def make_class(rows, cols, codes=None, suh=None, suh1=None, svh=None, dn_suh=None) -> Class:
+    """One class's tables from STACKED device tensors ([entries, ...], contiguous entries)."""
+    c = Class()
+    c.rows, c.cols = rows, cols
+    for name, t in (("codes", codes), ("suh", suh), ("suh1", suh1), ("svh", svh), ("dn_suh", dn_suh)):
+        if t is None:
+            setattr(c, name, None)
+            setattr(c, name + "_stride", 0)
+        else:
+            setattr(c, name, t.data_ptr())
+            setattr(c, name + "_stride", t.stride(0) * t.element_size())
+    return c
+
+
+def make_op(op, bits, cb, classes, x, sorted_tok, expert_offset, y, M, top_k, h_rot=0, a_rot=0, dn=None,
+            x_bf16=False, n_expert=None) -> Op:
+    o = Op()
+    o.op, o.bits, o.codebook = op, bits, CB.get(cb, cb)
+    o.n_class, o.h_rot, o.a_rot = len(classes), h_rot, a_rot
+    o.M, o.top_k = M, top_k
+    o.n_expert = expert_offset.numel() - 1 if n_expert is None else n_expert
+    for i, c in enumerate(classes):
+        o.cls[i] = c
+    for i, c in enumerate(dn or []):
+        o.dn[i] = c
+    o.x = x.data_ptr()
+    o.x_dtype = BF16 if x_bf16 else F16
+    o.x_rows, o.x_cols, o.x_pitch = x.shape[0], x.shape[1], x.stride(0)
+    o.sorted_tok, o.expert_offset = sorted_tok.data_ptr(), expert_offset.data_ptr()
+    o.y = y.data_ptr()
+    o.T, o.y_cols, o.y_pitch = y.shape[0], y.shape[1], y.stride(0)
+    return o
+
+
+def scratch_bytes(o: Op) -> int:
+    return int(lib().exl3c4_scratch_bytes(C.byref(o)))
+
+
+def launch(o: Op, scratch=None, stream=None) -> int:
+    """Runs one op; returns the status (0 OK). `scratch`: a uint8 device tensor of >= scratch_bytes(o)."""
+    n = 0 if scratch is None else scratch.numel()
+    return int(lib().exl3c4_launch(C.byref(o), _ptr(scratch), n, _stream(stream)))
+
+
+def alloc_scratch(o: Op, device="cuda"):
+    import torch
+    n = scratch_bytes(o)
+    if n < 0:
+        raise RuntimeError(f"exl3c4_scratch_bytes: {STATUS.get(n, n)}")
+    return torch.empty(max(n, 256), dtype=torch.uint8, device=device)

@@ -1,0 +1,195 @@
+"""cases.py -- random routed-expert cases shared by the oracle-level and the device parity tests.
+
+A case is numpy data only (canonical planes, scales, routing, activations). `oracle_*` run the CPU restatement;
+`Dev` uploads the case (codes through the library's own relayout, as a loader would) and runs the device ops through
+the C-ABI (radiance-exl3_amd/exl3c4.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import exl3c4_synth as syn
+import oracle
+
+
+class Expert:
+    def __init__(self, rng, rows, cols, bits, stacked, dn_width=None, suh_mag=1.0, svh_mag=None):
+        self.rows, self.cols, self.bits = rows, cols, bits
+        self.codes = syn.random_codes(rng, rows, cols, bits)
+        self.suh = syn.varied_scales(rng, cols, suh_mag)
+        self.suh1 = syn.varied_scales(rng, cols, suh_mag) if stacked else None
+        self.svh = syn.varied_scales(rng, rows, svh_mag if svh_mag else 1.0 / np.sqrt(cols))
+        self.dn_suh = None
+
+
+class Case:
+    """n_expert experts of n_class classes: gate_up [2W_c, H_c] and down [H_c, W_c] per expert, class c = e % n_class."""
+
+    def __init__(self, seed, n_tok, top_k, n_expert, geoms, bits, cb, drop=0.0, protect_tail=0, x_bf16=False,
+                 routing="uniform"):
+        rng = np.random.default_rng(seed)
+        self.rng = rng
+        self.n_tok, self.top_k, self.n_expert, self.bits, self.cb = n_tok, top_k, n_expert, bits, cb
+        self.n_class = len(geoms)
+        self.geoms = geoms                                  # per class (H, W): hidden, width
+        self.gu, self.dn = [], []
+        for e in range(n_expert):
+            H, W = geoms[e % self.n_class]
+            g = Expert(rng, 2 * W, H, bits, True)
+            d = Expert(rng, H, W, bits, False)
+            g.dn_suh = d.suh                                # down's suh of the same expert
+            self.gu.append(g)
+            self.dn.append(d)
+        Hmax = max(h for h, _ in geoms)
+        self.x_bf16 = x_bf16
+        x = rng.standard_normal((n_tok, Hmax)).astype(np.float32)
+        if x_bf16:
+            self.x = (x.view(np.uint32) >> 16).astype(np.uint16)          # bf16 bits (truncation: any bits are fine)
+        else:
+            self.x = x.astype(np.float16).view(np.uint16)
+        if routing == "zipf":
+            ids, w = syn.zipf_topk(rng, n_tok, n_expert, top_k)
+        else:
+            ids, w = syn.router_topk(rng.standard_normal((n_tok, n_expert)), top_k)
+        if drop:
+            kill = rng.random(ids.shape) < drop
+            ids = np.where(kill, -1, ids).astype(np.int32)
+        self.ids, self.w = ids, w
+        st, off = syn.moe_scatter(ids, n_expert)
+        if protect_tail:
+            # rows past the live count that hold valid flat indices (a `protect` sort): the ops must zero them
+            n_live = int(off[-1])
+            take = min(protect_tail, st.size - n_live)
+            st[n_live:n_live + take] = np.arange(take)
+        self.sorted_tok, self.off = st, off
+        self.T = st.size
+
+    # ------------------------------------------------------------------ class tables (numpy, stacked)
+    def classes(self, which):
+        out = []
+        for c in range(self.n_class):
+            ex = [(self.gu if which == "gu" else self.dn)[e] for e in range(c, self.n_expert, self.n_class)]
+            d = {"rows": ex[0].rows, "cols": ex[0].cols,
+                 "codes": np.stack([x.codes for x in ex]), "suh": np.stack([x.suh for x in ex]),
+                 "svh": np.stack([x.svh for x in ex])}
+            if which == "gu":
+                d["suh1"] = np.stack([x.suh1 for x in ex])
+                d["dn_suh"] = np.stack([x.dn_suh for x in ex])
+            out.append(d)
+        return out
+
+    # ------------------------------------------------------------------ the oracle
+    def oracle_prep(self, prefill=0xFFFF):
+        cl = self.classes("gu")
+        y = np.full((self.T, 2 * max(c["cols"] for c in cl)), prefill, np.uint16)
+        return oracle.run_op(oracle.OP_PREP_GU, cl, self.bits, self.cb, self.x, self.sorted_tok, self.off,
+                             self.top_k, x_bf16=self.x_bf16, y=y)
+
+    def oracle_gate_up(self, h_rot=0, a_rot=0, xr=None):
+        x = xr if a_rot else self.x
+        return oracle.run_op(oracle.OP_GATE_UP, self.classes("gu"), self.bits, self.cb, x, self.sorted_tok, self.off,
+                             self.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=self.x_bf16 and not a_rot)
+
+    def oracle_down(self, h, h_rot=0):
+        return oracle.run_op(oracle.OP_DOWN, self.classes("dn"), self.bits, self.cb, h, self.sorted_tok, self.off,
+                             self.top_k, h_rot=h_rot)
+
+    def oracle_gate_up_down(self):
+        return oracle.run_gate_up_down(self.classes("gu"), self.classes("dn"), self.bits, self.cb, self.x,
+                                       self.sorted_tok, self.off, self.top_k, x_bf16=self.x_bf16)
+
+
+def f16(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+def bf16(bits):
+    return syn.bf16_to_f32(bits)
+
+
+def rel_err(got, want):
+    """max-abs error over RMS of the reference output (the north star's criterion: <= 2e-3)."""
+    rms = float(np.sqrt(np.mean(want.astype(np.float64) ** 2)))
+    return float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64)))) / max(rms, 1e-30)
+
+
+class Dev:
+    """A case uploaded to the device: stacked stored records and scales, routing, activations."""
+
+    def __init__(self, case: Case):
+        import torch
+        import exl3c4
+        self.case = case
+        self.torch, self.ex = torch, exl3c4
+        dev = "cuda"
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        self.tabs = {}
+        for which in ("gu", "dn"):
+            cls = []
+            for c in case.classes(which):
+                recs = np.stack([exl3c4.relayout(codes, c["rows"], c["cols"], case.bits) for codes in c["codes"]])
+                d = {"rows": c["rows"], "cols": c["cols"], "codes": t(recs),
+                     "suh": t(c["suh"].view(np.uint16)), "svh": t(c["svh"].view(np.uint16))}
+                if which == "gu":
+                    d["suh1"] = t(c["suh1"].view(np.uint16))
+                    d["dn_suh"] = t(c["dn_suh"].view(np.uint16))
+                cls.append(d)
+            self.tabs[which] = cls
+        self.x = t(case.x.astype(np.uint16).view(np.int16))
+        self.sorted_tok = t(case.sorted_tok)
+        self.off = t(case.off)
+
+    def cls(self, which, dn_suh=True):
+        out = []
+        for d in self.tabs[which]:
+            out.append(self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], suh=d["suh"], suh1=d.get("suh1"),
+                                          svh=d["svh"], dn_suh=d.get("dn_suh") if dn_suh else None))
+        return out
+
+    def _run(self, o, expect=0):
+        s = self.ex.alloc_scratch(o)
+        rc = self.ex.launch(o, s)
+        assert rc == expect, f"launch status {self.ex.STATUS.get(rc, rc)}"
+        self.torch.cuda.synchronize()
+
+    def out(self, cols, fill=0x7E7E):
+        return self.torch.full((self.case.T, cols), fill, dtype=self.torch.int16, device="cuda")
+
+    def prep(self, prefill=0xFFFF):
+        c = self.case
+        C = max(d["cols"] for d in self.tabs["gu"])
+        y = self.out(2 * C, fill=np.int16(np.uint16(prefill).view(np.int16)))
+        o = self.ex.make_op(self.ex.PREP_GU, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
+                            c.n_tok, c.top_k, x_bf16=c.x_bf16)
+        self._run(o)
+        return y.cpu().numpy().view(np.uint16)
+
+    def gate_up(self, h_rot=0, a_rot=0, xr=None):
+        c = self.case
+        W = max(d["rows"] for d in self.tabs["gu"]) // 2
+        y = self.out(W)
+        x = xr if a_rot else self.x
+        o = self.ex.make_op(self.ex.GATE_UP, c.bits, c.cb, self.cls("gu"), x, self.sorted_tok, self.off, y,
+                            c.n_tok, c.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=c.x_bf16 and not a_rot)
+        self._run(o)
+        return y.cpu().numpy().view(np.uint16)
+
+    def down(self, h, h_rot=0):
+        c = self.case
+        N = max(d["rows"] for d in self.tabs["dn"])
+        y = self.out(N)
+        hd = self.torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).to("cuda")
+        o = self.ex.make_op(self.ex.DOWN, c.bits, c.cb, self.cls("dn"), hd, self.sorted_tok, self.off, y,
+                            c.n_tok, c.top_k, h_rot=h_rot)
+        self._run(o)
+        return y.cpu().numpy().view(np.uint16)
+
+    def gate_up_down(self):
+        c = self.case
+        N = max(d["rows"] for d in self.tabs["dn"])
+        y = self.out(N)
+        dn = [self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in self.tabs["dn"]]
+        o = self.ex.make_op(self.ex.GU_DN, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
+                            c.n_tok, c.top_k, dn=dn, x_bf16=c.x_bf16)
+        self._run(o)
+        return y.cpu().numpy().view(np.uint16)

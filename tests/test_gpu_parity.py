@@ -1,0 +1,144 @@
+"""Device parity: libexl3c4.so's HIP kernels, called through the C-ABI, against the CPU oracle (oracle/exl3_oracle.c).
+
+Bars (the north star's): W_hat bit-exact with the reference decode; prep_gu's xr bit-exact (the same f32 butterfly and
+roundings); op outputs within max-abs <= 2e-3 * RMS(output) of the oracle (fp16 in, fp32 accumulate, the MFMA's
+summation order); and, to the bit, the contract's invariants: the h_rot pair equal across the flag, prep_gu ->
+gate_up(a_rot 1) equal to gate_up(a_rot 0), gate_up_down equal to its pair, zero rows, prep_gu's unwritten regions,
+replay determinism.
+"""
+import numpy as np
+import pytest
+
+from cases import Case, Dev, bf16, f16, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import exl3c4
+    exl3c4.lib()          # raises if the library is not built: no fallback exists
+    return torch
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------------------------------ dequant, bit-exact
+@pytest.mark.parametrize("bits", range(1, 9))
+@pytest.mark.parametrize("cb", ["mul1", "mcg", "3inst"])
+def test_dequant_is_bit_exact_against_the_oracle(torch_cuda, bits, cb):
+    import exl3c4
+    import exl3c4_synth as syn
+    import oracle
+    torch = torch_cuda
+    rows, cols = 128, 256
+    _say(f"dequant K={bits} {cb} [{rows}x{cols}]")
+    rng = np.random.default_rng(1000 + bits)
+    codes = syn.random_codes(rng, rows, cols, bits)
+    rec = torch.from_numpy(exl3c4.relayout(codes, rows, cols, bits)).cuda()
+    got = exl3c4.dequant(rec, rows, cols, bits, cb).cpu().numpy().view(np.uint16)
+    want = oracle.what_rows(codes, rows, cols, bits, cb, f16=True)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {want.size} differ"
+
+
+def test_dequant_covers_every_mul1_state_at_the_expert_geometry(torch_cuda):
+    """A whole gate_up weight [1024 x 2048] at K=4 visits (nearly) all 65,536 states; every W_hat bit equal."""
+    import exl3c4
+    import exl3c4_synth as syn
+    import oracle
+    torch = torch_cuda
+    rows, cols, bits = 1024, 2048, 4
+    _say("dequant K=4 mul1 [1024x2048]")
+    rng = np.random.default_rng(77)
+    codes = syn.random_codes(rng, rows, cols, bits)
+    rec = torch.from_numpy(exl3c4.relayout(codes, rows, cols, bits)).cuda()
+    got = exl3c4.dequant(rec, rows, cols, bits, "mul1").cpu().numpy().view(np.uint16)
+    want = oracle.what_rows(codes, rows, cols, bits, "mul1", f16=True)
+    assert np.array_equal(got, want)
+    table = oracle.codebook_table("mul1")
+    assert np.unique(want).size == np.unique(table).size      # every value the codebook has occurs
+
+
+# ------------------------------------------------------------------------------------------ the ops
+SMALL = dict(n_tok=4, top_k=4, n_expert=8, geoms=[(256, 128)], bits=4, cb="mul1")
+
+
+def _check_all(case, label):
+    dev = Dev(case)
+    _say(f"{label}: prep_gu")
+    xr_d = dev.prep()
+    xr_o = case.oracle_prep()
+    assert np.array_equal(xr_d, xr_o), f"prep_gu: {np.count_nonzero(xr_d != xr_o)} elements differ"
+
+    _say(f"{label}: gate_up h_rot 0 / 1, a_rot 0 / 1")
+    h0 = dev.gate_up(h_rot=0)
+    h0_o = case.oracle_gate_up(h_rot=0)
+    assert rel_err(f16(h0), f16(h0_o)) <= TOL
+    h1 = dev.gate_up(h_rot=1)
+    assert rel_err(f16(h1), f16(case.oracle_gate_up(h_rot=1))) <= TOL
+    xr_t = dev.torch.from_numpy(xr_d.view(np.int16)).cuda()
+    assert np.array_equal(dev.gate_up(h_rot=0, a_rot=1, xr=xr_t), h0)          # prep_gu -> gate_up(a_rot 1): same bits
+    assert np.array_equal(dev.gate_up(h_rot=1, a_rot=1, xr=xr_t), h1)
+
+    _say(f"{label}: down h_rot 0 / 1, gate_up_down")
+    y0 = dev.down(h0, h_rot=0)
+    y0_o = case.oracle_down(h0, h_rot=0)               # the oracle's down on the DEVICE's h: isolates down
+    assert rel_err(bf16(y0), bf16(y0_o)) <= TOL
+    y1 = dev.down(h1, h_rot=1)
+    assert np.array_equal(y1, y0)                      # the pair's bits do not depend on h_rot
+    gd = dev.gate_up_down()
+    assert np.array_equal(gd, y1)                      # gate_up_down is its pair, to the bit
+    gd_o = case.oracle_gate_up_down()
+    assert rel_err(bf16(gd), bf16(gd_o)) <= TOL
+
+    # zero rows: dropped slots, rows past the live count (whatever sorted_tok holds there), outside the runs
+    T, live = case.T, int(case.off[-1])
+    dead = np.array([i >= live or i < case.off[0] or case.sorted_tok[i] < 0 for i in range(T)])
+    for out in (h0, h1, y0, gd):
+        assert np.all(out[dead] == 0)
+    # determinism: a replay writes the same bytes
+    assert np.array_equal(dev.gate_up_down(), gd)
+    return dev
+
+
+def test_ops_small_case(torch_cuda):
+    _check_all(Case(seed=1, **SMALL), "small")
+
+
+def test_ops_two_classes_of_different_width_with_drops_and_protected_rows(torch_cuda):
+    case = Case(seed=2, n_tok=6, top_k=3, n_expert=9, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
+                drop=0.2, protect_tail=2)
+    _check_all(case, "two-class")
+
+
+def test_ops_bf16_input(torch_cuda):
+    _check_all(Case(seed=3, x_bf16=True, **{**SMALL, "n_expert": 5}), "bf16")
+
+
+@pytest.mark.parametrize("bits,cb", [(2, "mul1"), (3, "mcg"), (5, "3inst"), (6, "mul1"), (7, "mcg"), (8, "mul1")])
+def test_ops_every_k_and_codebook(torch_cuda, bits, cb):
+    _check_all(Case(seed=10 + bits, n_tok=3, top_k=2, n_expert=4, geoms=[(128, 128)], bits=bits, cb=cb),
+               f"K={bits} {cb}")
+
+
+def test_ops_four_classes(torch_cuda):
+    case = Case(seed=5, n_tok=5, top_k=4, n_expert=11, geoms=[(256, 128), (256, 256), (128, 128), (256, 128)],
+                bits=3, cb="mul1")
+    _check_all(case, "four-class")
+
+
+@pytest.mark.parametrize("bits", [3, 4, 5])
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_single_routed_expert_at_the_baseline_geometry(torch_cuda, bits, m):
+    """one SwiGLU expert, gate/up 2048 -> 512, down 512 -> 2048, m tokens, top_k = 1."""
+    case = Case(seed=20 + bits * 100 + m, n_tok=m, top_k=1, n_expert=1, geoms=[(2048, 512)], bits=bits, cb="mul1")
+    dev = Dev(case)
+    _say(f"single expert K={bits} m={m}")
+    gd = dev.gate_up_down()
+    assert rel_err(bf16(gd), bf16(case.oracle_gate_up_down())) <= TOL
