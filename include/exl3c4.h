@@ -107,6 +107,26 @@ int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
  * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* The kernels one launch runs, in order (gate_up_down runs all but a prep_gu op's prep; down runs prep only at
+ * h_rot = 0; gate_up runs prep only at a_rot = 0). */
+enum { EXL3C4_K_PLAN = 0, EXL3C4_K_PREP = 1, EXL3C4_K_GEMV_GU = 2, EXL3C4_K_EPI_GU = 3, EXL3C4_K_GEMV_DN = 4,
+       EXL3C4_K_EPI_DN = 5 };
+
+/* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and
+ * ev_stop (two hipEvent_t the caller created) at its start and end: the duration of that one kernel, read with
+ * hipEventElapsedTime, however the host paces the launches. A measurement entry with no counterpart in the reference
+ * (whose device library times kernels with compile-time timestamp arms, kernels/exl3r4d/exl3r4d.hip:135-136); the bits
+ * written are exl3c4_launch's. */
+int exl3c4_launch_timed(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
+                        void* ev_start, void* ev_stop);
+
+/* Where a launch of `op` leaves the f32 partial sums of its GEMM (gemm 0: gate_up's, or down's for the down op; 1:
+ * gate_up_down's down) in its scratch: acc[row][col] = sum over s < *splits of the f32 at scratch + *offset +
+ * 4 * (s * *split_stride + row * *pitch + col), for the live rows. The epilogue adds them in this order. For a checker
+ * of the accumulation itself (the values before any narrowing); no counterpart in the reference. */
+int exl3c4_scratch_partials(const Exl3c4Op* op, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,
+                            int32_t* splits);
+
 /* W_hat of one stored weight [rows, cols] as fp16 bits [rows][w_pitch] on the device -- the same decode the GEMMs run,
  * exposed so it can be compared bit for bit with common/exl3_decode.c:193-221. bits 1..8 (K = 1 is decoder-only,
  * include/exl3_encoding.h:45-48). */

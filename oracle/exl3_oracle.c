@@ -339,6 +339,12 @@ static void prologue(const float* x, const uint16_t* s, int64_t cols, float* xr)
     for (int64_t k = 0; k < cols; ++k) xr[k] = h2f(f2h(xr[k]));
 }
 
+int or_prologue(const float* x, const uint16_t* s, int64_t n, float* xr) {
+    if (!x || !s || !xr || n % 128) return OR_E_SHAPE;
+    prologue(x, s, n, xr);
+    return OR_OK;
+}
+
 /* kernels/exl3ref/ref.c:35-42: acc[n] = sum over ascending k of xr[k] * what[n][k], one product and one add. */
 static void gemv(const float* xr, const float* what, int64_t rows, int64_t cols, float* acc) {
     for (int64_t n = 0; n < rows; ++n) {

@@ -105,6 +105,9 @@ typedef struct OrOp {
  * checked). Returns OR_OK, or OR_E_SHAPE / OR_E_NOMEM. */
 int or_launch(const OrOp* o);
 
+/* kernels/exl3ref/ref.c:27-32: xr = f16(had(f16(x * s))) over n values (x f32, s f16 bits), as f32. */
+int or_prologue(const float* x, const uint16_t* s, int64_t n, float* xr);
+
 /* gate_up(a_rot 0, h_rot 1) then down(h_rot 1): the gate_up_down definition (kernels/exl3ref/ref.c:235-276).
  * `gu` is the gate_up op (its y unused), `dn` the down op (its x unused); h is allocated here. */
 int or_gate_up_down(const OrOp* gu, const OrOp* dn);

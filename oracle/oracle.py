@@ -83,6 +83,8 @@ def _declare(L):
     L.or_gate_up_down.restype = C.c_int
     L.or_gate_up_down.argtypes = [_p, _p]
     L.or_moe_scatter.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p]
+    L.or_prologue.restype = C.c_int
+    L.or_prologue.argtypes = [_p, _p, _i64, _p]
 
 
 def _ptr(a: np.ndarray):
@@ -210,6 +212,16 @@ def decode_rows(codes, rows, cols, bits, cb, suh, svh, suh1=None, row0=0, n=None
                               None if s1 is None else _ptr(s1), _ptr(svh), row0, n, _ptr(out))
     if rc:
         raise ValueError(f"decode_rows rc={rc}")
+    return out
+
+
+def prologue(x: np.ndarray, s: np.ndarray) -> np.ndarray:
+    """f16(had128(f16(x * s))) as f32 (kernels/exl3ref/ref.c:27-32); x f32 [n], s f16 [n]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    s = np.ascontiguousarray(s).view(np.uint16)
+    out = np.zeros_like(x)
+    if lib().or_prologue(_ptr(x), _ptr(s), x.size, _ptr(out)):
+        raise ValueError("prologue needs a multiple of 128")
     return out
 
 

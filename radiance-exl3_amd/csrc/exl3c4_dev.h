@@ -40,11 +40,12 @@ typedef struct Exl3c4Launch {
 /* prep modes */
 enum { EXL3C4_PREP_GU_SCRATCH = 0, EXL3C4_PREP_GU_OP = 1, EXL3C4_PREP_DN = 2 };
 
-/* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. */
-int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream);
-int exl3c4_dev_prep(const Exl3c4Launch* a, int halves, void* stream);
-int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream);
-int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream);
+/* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the
+ * dispatch itself stamps at its start and end (hipExtLaunchKernelGGL), or null for a plain launch. */
+int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_prep(const Exl3c4Launch* a, int halves, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
                        int64_t w_pitch, void* stream);
 

@@ -24,6 +24,7 @@
 // state's half), so no state is ever masked; the byte sum lands as fp16 bits 0x6400 + s through v_sad_u8 /
 // v_sad_hi_u8 for two weights at once, and one v_pk_fma_f16 forms (1024 + s) * K_INV + K_BIAS for both with one
 // rounding each -- exactly common/exl3_decode.c:47-58.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
@@ -50,7 +51,13 @@ __device__ __forceinline__ const void* tab_entry(const void* base, int64_t strid
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// f32 -> f16, round to nearest even, of an f32 VALUE. The empty asm makes the operand a materialised f32 register:
+// without it the backend folds a producing multiply into v_fma_mixlo_f16, which rounds the exact product to f16 once,
+// where the reference rounds it to f32 first (a tie then lands on the other side, as measured on gfx950).
+__device__ __forceinline__ uint16_t f2h(float f) {
+    asm volatile("" : "+v"(f));
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // round to nearest even on the f32 bits (radiance's rad_f32_to_bf16); a nan stays a quiet nan
 __device__ __forceinline__ uint16_t f2bf(float f) {
@@ -496,36 +503,42 @@ DequantFn pick_dequant(int bits, int cb) {
 
 int launched(void) { return hipGetLastError() == hipSuccess ? 0 : EXL3C4_E_DEVICE; }
 
+// A plain launch, or one whose dispatch stamps two events at its own start and end (the timing of one kernel).
+template <typename F, typename... Args>
+int go(F f, unsigned blocks, hipStream_t s, void* ev0, void* ev1, Args... args) {
+    if (ev0 && ev1)
+        hipExtLaunchKernelGGL(f, dim3(blocks), dim3(256), 0, s, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, args...);
+    else
+        hipLaunchKernelGGL(f, dim3(blocks), dim3(256), 0, s, args...);
+    return launched();
+}
+
 unsigned blocks_for_waves(int64_t waves) { return (unsigned)((waves + 3) / 4); }
 
 }  // namespace
 
-extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream) {
-    hipLaunchKernelGGL(k_plan, dim3(1), dim3(256), 0, (hipStream_t)stream, *a);
-    return launched();
+extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    return go(k_plan, 1, (hipStream_t)stream, ev0, ev1, *a);
 }
 
-extern "C" int exl3c4_dev_prep(const Exl3c4Launch* a, int halves, void* stream) {
+extern "C" int exl3c4_dev_prep(const Exl3c4Launch* a, int halves, void* stream, void* ev0, void* ev1) {
     const int64_t waves = (int64_t)a->T * halves;
     if (waves <= 0) return 0;
-    hipLaunchKernelGGL(k_prep, dim3(blocks_for_waves(waves)), dim3(256), 0, (hipStream_t)stream, *a, halves);
-    return launched();
+    return go(k_prep, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a, halves);
 }
 
-extern "C" int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream) {
+extern "C" int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const GemvFn f = pick_gemv(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     const int64_t waves = (int64_t)a->max_chunks * a->max_strips * a->ksplit;
     if (waves <= 0) return 0;
-    hipLaunchKernelGGL(f, dim3(blocks_for_waves(waves)), dim3(256), 0, (hipStream_t)stream, *a);
-    return launched();
+    return go(f, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
-extern "C" int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream) {
+extern "C" int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const int64_t waves = (int64_t)a->T * (a->y_cols / 128);
     if (waves <= 0) return 0;
-    hipLaunchKernelGGL(k_epilogue, dim3(blocks_for_waves(waves)), dim3(256), 0, (hipStream_t)stream, *a);
-    return launched();
+    return go(k_epilogue, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

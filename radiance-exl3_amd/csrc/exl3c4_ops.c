@@ -198,7 +198,11 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->x_rows = (int32_t)o->x_rows;
 }
 
-int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
+/* The events of a timed launch go to exactly one kernel of the sequence. */
+typedef struct Timed { int kernel; void *ev0, *ev1; } Timed;
+#define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
+
+static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     if ((rc = check(o)) != EXL3C4_OK) return rc;
@@ -217,16 +221,16 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
         a.x = o->x; a.x_pitch = o->x_pitch;
         a.y = o->y; a.y_pitch = o->y_pitch;
         a.prep_mode = EXL3C4_PREP_GU_OP;
-        return exl3c4_dev_prep(&a, 2, stream);
+        return exl3c4_dev_prep(&a, 2, stream, EV(EXL3C4_K_PREP));
     }
-    if ((rc = exl3c4_dev_plan(&a, stream)) != 0) return rc;
+    if ((rc = exl3c4_dev_plan(&a, stream, EV(EXL3C4_K_PLAN))) != 0) return rc;
 
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         if (op == EXL3C4_GU_DN || !o->a_rot) {
             a.x = o->x; a.x_pitch = o->x_pitch;
             a.y = s + k.xr; a.y_pitch = k.xr_pitch;
             a.prep_mode = EXL3C4_PREP_GU_SCRATCH;
-            if ((rc = exl3c4_dev_prep(&a, 2, stream)) != 0) return rc;
+            if ((rc = exl3c4_dev_prep(&a, 2, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
             a.a = s + k.xr; a.a_pitch = k.xr_pitch;
         } else {
             a.a = o->x; a.a_pitch = o->x_pitch;
@@ -234,15 +238,15 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
         a.gate_up = 1;
         a.ksplit = k.split_gu;
         a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
-        if ((rc = exl3c4_dev_gemv(&a, stream)) != 0) return rc;
+        if ((rc = exl3c4_dev_gemv(&a, stream, EV(EXL3C4_K_GEMV_GU))) != 0) return rc;
         if (op == EXL3C4_GATE_UP) {
             a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
             a.h_rot = o->h_rot;
-            return exl3c4_dev_epilogue(&a, stream);
+            return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU));
         }
         a.y = s + k.h; a.y_pitch = k.h_pitch; a.y_cols = (int32_t)k.h_pitch;
         a.h_rot = 1;
-        if ((rc = exl3c4_dev_epilogue(&a, stream)) != 0) return rc;
+        if ((rc = exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
         /* down over h: gate_up_down's down classes [cols, rows / 2], suh = gate_up's dn_suh (include/exl3_abi.h:
          * 751-800); h crosses rotated (h_rot = 1) */
         Exl3c4Launch d;
@@ -260,9 +264,9 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
         d.gate_up = 0;
         d.ksplit = k.split_dn;
         d.max_strips = (int32_t)(nmax / EXL3C4_STRIP);
-        if ((rc = exl3c4_dev_gemv(&d, stream)) != 0) return rc;
+        if ((rc = exl3c4_dev_gemv(&d, stream, EV(EXL3C4_K_GEMV_DN))) != 0) return rc;
         d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
-        return exl3c4_dev_epilogue(&d, stream);
+        return exl3c4_dev_epilogue(&d, stream, EV(EXL3C4_K_EPI_DN));
     }
 
     /* down */
@@ -270,7 +274,7 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
         a.x = o->x; a.x_pitch = o->x_pitch;
         a.y = s + k.xr; a.y_pitch = k.xr_pitch;
         a.prep_mode = EXL3C4_PREP_DN;
-        if ((rc = exl3c4_dev_prep(&a, 1, stream)) != 0) return rc;
+        if ((rc = exl3c4_dev_prep(&a, 1, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
         a.a = s + k.xr; a.a_pitch = k.xr_pitch;
     } else {
         a.a = o->x; a.a_pitch = o->x_pitch;
@@ -279,9 +283,36 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
     a.gate_up = 0;
     a.ksplit = k.split_dn;
     a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
-    if ((rc = exl3c4_dev_gemv(&a, stream)) != 0) return rc;
+    if ((rc = exl3c4_dev_gemv(&a, stream, EV(EXL3C4_K_GEMV_DN))) != 0) return rc;
     a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
-    return exl3c4_dev_epilogue(&a, stream);
+    return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_DN));
+}
+
+int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
+    const Timed t = { -1, NULL, NULL };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
+}
+
+int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
+                        void* ev_start, void* ev_stop) {
+    if (kernel < EXL3C4_K_PLAN || kernel > EXL3C4_K_EPI_DN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
+    const Timed t = { kernel, ev_start, ev_stop };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
+}
+
+int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,
+                            int32_t* splits) {
+    int rc;
+    if (!o || !offset || !pitch || !split_stride || !splits) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    if (o->op == EXL3C4_PREP_GU || (gemm == 1 && o->op != EXL3C4_GU_DN) || gemm < 0 || gemm > 1) return EXL3C4_E_INVAL;
+    Carve k;
+    carve(o, o->T, &k);
+    *offset = k.part;
+    *pitch = k.part_pitch;
+    *split_stride = k.T * k.part_pitch;
+    *splits = (o->op == EXL3C4_DOWN || gemm == 1) ? k.split_dn : k.split_gu;
+    return EXL3C4_OK;
 }
 
 int exl3c4_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,

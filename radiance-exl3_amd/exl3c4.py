@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libexl3c4.so")
 
 DOWN, GATE_UP, PREP_GU, GU_DN = 0, 1, 2, 3
+K_PLAN, K_PREP, K_GEMV_GU, K_EPI_GU, K_GEMV_DN, K_EPI_DN = 0, 1, 2, 3, 4, 5
 CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 F16, BF16 = 0, 1
 STATUS = {0: "OK", -1: "RAD_E_SHAPE", -2: "RAD_E_DTYPE", -3: "RAD_E_ALIGN", -4: "RAD_E_STRIDE", -9: "RAD_E_SCHEMA",
@@ -61,6 +62,11 @@ def lib():
         L.exl3c4_relayout.argtypes = [_p, _i64, _i64, _i64, _i32, _p]
         L.exl3c4_unrelayout.restype = C.c_int
         L.exl3c4_unrelayout.argtypes = [_p, _i64, _i64, _i32, _p, _i64]
+        L.exl3c4_launch_timed.restype = C.c_int
+        L.exl3c4_launch_timed.argtypes = [C.POINTER(Op), _p, _i64, _p, _i32, _p, _p]
+        L.exl3c4_scratch_partials.restype = C.c_int
+        L.exl3c4_scratch_partials.argtypes = [C.POINTER(Op), _i32, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64),
+                                              C.POINTER(_i32)]
         L.exl3c4_build_target.restype = C.c_char_p
         L.exl3c4_abi_version.restype = C.c_int
         _lib = L
@@ -97,6 +103,61 @@ def _stream(stream):
 
 def _ptr(t):
     return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def ptr(t):
+    return _ptr(t)
+
+
+def ctypes_ref(o: Op):
+    return C.byref(o)
+
+
+def stream_handle(stream=None):
+    return _stream(stream)
+
+
+# ------------------------------------------------------------------------------------------ HIP events (timing)
+_hip = None
+
+
+def hip():
+    """The HIP runtime libexl3c4.so links, for events the caller owns (hipEventCreate / ElapsedTime)."""
+    global _hip
+    if _hip is None:
+        lib()
+        _hip = C.CDLL("libamdhip64.so")
+        _hip.hipEventCreate.argtypes = [C.POINTER(_p)]
+        _hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), _p, _p]
+        _hip.hipEventDestroy.argtypes = [_p]
+    return _hip
+
+
+class Event:
+    """A raw hipEvent_t (created at once, so a dispatch can stamp it)."""
+
+    def __init__(self):
+        self.h = _p()
+        if hip().hipEventCreate(C.byref(self.h)):
+            raise RuntimeError("hipEventCreate failed")
+
+    def __del__(self):
+        if _hip is not None and self.h:
+            _hip.hipEventDestroy(self.h)
+
+
+def elapsed_ms(a: Event, b: Event) -> float:
+    ms = C.c_float()
+    if hip().hipEventElapsedTime(C.byref(ms), a.h, b.h):
+        raise RuntimeError("hipEventElapsedTime failed")
+    return float(ms.value)
+
+
+def launch_timed(o: Op, scratch, kernel: int, ev_start: Event, ev_stop: Event, stream=None) -> int:
+    """exl3c4_launch with kernel `kernel` stamping ev_start / ev_stop at its own start and end."""
+    n = 0 if scratch is None else scratch.numel()
+    return int(lib().exl3c4_launch_timed(C.byref(o), _ptr(scratch), n, _stream(stream), kernel, ev_start.h,
+                                         ev_stop.h))
 
 
 def dequant(record, rows: int, cols: int, bits: int, cb, stream=None):
@@ -151,6 +212,22 @@ def launch(o: Op, scratch=None, stream=None) -> int:
     """Runs one op; returns the status (0 OK). `scratch`: a uint8 device tensor of >= scratch_bytes(o)."""
     n = 0 if scratch is None else scratch.numel()
     return int(lib().exl3c4_launch(C.byref(o), _ptr(scratch), n, _stream(stream)))
+
+
+def partial_sums(o: Op, scratch, gemm: int = 0):
+    """The f32 accumulations a launch left in `scratch` (torch tensor), splits added in the epilogue's order:
+    float32 numpy [T, pitch]."""
+    off, pitch, ss, n = _i64(), _i64(), _i64(), _i32()
+    rc = lib().exl3c4_scratch_partials(C.byref(o), gemm, C.byref(off), C.byref(pitch), C.byref(ss), C.byref(n))
+    if rc:
+        raise RuntimeError(f"exl3c4_scratch_partials: {STATUS.get(rc, rc)}")
+    raw = scratch.cpu().numpy()[off.value:].view(np.float32)
+    T = o.T
+    acc = raw[: T * pitch.value].reshape(T, pitch.value).copy()
+    for s in range(1, n.value):      # columns no launch wrote hold whatever scratch held: no float warnings for them
+        with np.errstate(over="ignore", invalid="ignore"):
+            acc = (acc + raw[s * ss.value: s * ss.value + T * pitch.value].reshape(T, pitch.value)).astype(np.float32)
+    return acc
 
 
 def alloc_scratch(o: Op, device="cuda"):

@@ -94,6 +94,55 @@ class Case:
         return oracle.run_op(oracle.OP_DOWN, self.classes("dn"), self.bits, self.cb, h, self.sorted_tok, self.off,
                              self.top_k, h_rot=h_rot)
 
+    def h_rot_of(self, h0):
+        """What gate_up's h_rot = 1 output must be, to the bit, given its h_rot = 0 output h0: down's first step
+        f16(had(f16(h0 * dn_suh))) on each live row (docs/OPS-exl3.md:120-123), zeros elsewhere."""
+        out = np.zeros_like(h0)
+        for i in range(self.T):
+            if i < self.off[0] or i >= self.off[-1] or self.sorted_tok[i] < 0:
+                continue
+            e = int(np.searchsorted(self.off, i, side="right") - 1)
+            g = self.gu[e]
+            W = g.rows // 2
+            xr = oracle.prologue(f16(h0[i, :W]), g.dn_suh)
+            out[i, :W] = xr.astype(np.float16).view(np.uint16)
+        return out
+
+    def live_rows(self):
+        """{expert: [rows]} of the rows an op computes: inside the runs, sorted_tok >= 0."""
+        rows = {}
+        for i in range(self.T):
+            if i < self.off[0] or i >= self.off[-1] or self.sorted_tok[i] < 0:
+                continue
+            rows.setdefault(int(np.searchsorted(self.off, i, side="right") - 1), []).append(i)
+        return rows
+
+    def oracle_gu_acc(self, xr):
+        """gate_up's f32 accumulations (before the output rotation) for every live row: [T, max N], zeros elsewhere."""
+        N = max(g.rows for g in self.gu)
+        out = np.zeros((self.T, N), np.float32)
+        for e, rows in self.live_rows().items():
+            g = self.gu[e]
+            what = oracle.what_rows(g.codes, g.rows, g.cols, self.bits, self.cb)
+            W, C = g.rows // 2, g.cols
+            x = f16(xr[rows])
+            out[rows, :W] = oracle_acc(x[:, :C], what[:W])
+            out[rows, W:2 * W] = oracle_acc(x[:, C:2 * C], what[W:])
+        return out
+
+    def oracle_dn_acc(self, h, h_rot):
+        """down's f32 accumulations on h (rotated first with down's suh when h_rot = 0): [T, max N]."""
+        N = max(d.rows for d in self.dn)
+        out = np.zeros((self.T, N), np.float32)
+        for e, rows in self.live_rows().items():
+            d = self.dn[e]
+            what = oracle.what_rows(d.codes, d.rows, d.cols, self.bits, self.cb)
+            x = f16(h[rows, :d.cols])
+            if not h_rot:
+                x = np.stack([oracle.prologue(r, d.suh) for r in x])
+            out[rows, :d.rows] = oracle_acc(x, what)
+        return out
+
     def oracle_gate_up_down(self):
         return oracle.run_gate_up_down(self.classes("gu"), self.classes("dn"), self.bits, self.cb, self.x,
                                        self.sorted_tok, self.off, self.top_k, x_bf16=self.x_bf16)
@@ -105,6 +154,40 @@ def f16(bits):
 
 def bf16(bits):
     return syn.bf16_to_f32(bits)
+
+
+def rel_l2(got, want):
+    """relative L2 (the reference's device criterion, tests/ref/test_exl3ref.py:336-346: <= 4e-3)."""
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    return float(np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30))
+
+
+def ordered(bits):
+    """fp16 / bf16 bit patterns as integers whose difference counts representable values (ulps) between them."""
+    b = np.asarray(bits, np.uint16).astype(np.int32)
+    return np.where(b & 0x8000, 0x8000 - b, b)
+
+
+def narrowed_ok(got, want, fmt):
+    """An output narrowed to f16 / bf16 agrees with the oracle's: every element within one unit in the last place of
+    its format (a summation order that differs in the f32 rounding can move a value across one rounding boundary) or
+    within 1e-4 x RMS in absolute terms (values near zero after cancellation, where an ulp is tiny). Returns the
+    number of elements outside the bound."""
+    g = f16(got) if fmt == "f16" else bf16(got)
+    w = f16(want) if fmt == "f16" else bf16(want)
+    rms = float(np.sqrt(np.mean(w.astype(np.float64) ** 2)))
+    ulp = np.abs(ordered(got) - ordered(want))
+    bad = (ulp > 1) & (np.abs(g.astype(np.float64) - w) > 1e-4 * rms)
+    return int(np.count_nonzero(bad))
+
+
+def oracle_acc(xr, what):
+    """acc[r, n] = sum over ascending k of xr[r, k] * what[n, k] in f32, one product and one add a step
+    (kernels/exl3ref/ref.c:35-42)."""
+    acc = np.zeros((xr.shape[0], what.shape[0]), np.float32)
+    for k in range(xr.shape[1]):
+        acc = (acc + (xr[:, k:k + 1] * what[None, :, k]).astype(np.float32)).astype(np.float32)
+    return acc
 
 
 def rel_err(got, want):
@@ -151,6 +234,12 @@ class Dev:
         rc = self.ex.launch(o, s)
         assert rc == expect, f"launch status {self.ex.STATUS.get(rc, rc)}"
         self.torch.cuda.synchronize()
+        self.last = (o, s)
+
+    def last_acc(self, gemm=0):
+        """The f32 accumulations the last launch left in its scratch."""
+        o, s = self.last
+        return self.ex.partial_sums(o, s, gemm)
 
     def out(self, cols, fill=0x7E7E):
         return self.torch.full((self.case.T, cols), fill, dtype=self.torch.int16, device="cuda")

@@ -1,18 +1,21 @@
 """Device parity: libexl3c4.so's HIP kernels, called through the C-ABI, against the CPU oracle (oracle/exl3_oracle.c).
 
-Bars (the north star's): W_hat bit-exact with the reference decode; prep_gu's xr bit-exact (the same f32 butterfly and
-roundings); op outputs within max-abs <= 2e-3 * RMS(output) of the oracle (fp16 in, fp32 accumulate, the MFMA's
-summation order); and, to the bit, the contract's invariants: the h_rot pair equal across the flag, prep_gu ->
-gate_up(a_rot 1) equal to gate_up(a_rot 0), gate_up_down equal to its pair, zero rows, prep_gu's unwritten regions,
-replay determinism.
+Bars: W_hat bit-exact with the reference decode; prep_gu's xr bit-exact (the same f32 butterfly and roundings); every
+op's output within max-abs <= 2e-3 * RMS(output) of the oracle run on the SAME inputs (the north star's bar, fp16 in,
+fp32 accumulate in the MFMA's summation order); the whole chain (gate_up_down) within relative L2 <= 4e-3 of the
+oracle's chain (the reference's device criterion, tests/ref/test_exl3ref.py:336-346 -- max-abs cannot hold there:
+a one-ulp f16 flip of h at an element ten times h's RMS, which summation order alone causes, is spread by the h_rot
+rotation); and, to the bit, the contract's invariants: the h_rot pair equal across the flag, prep_gu -> gate_up(a_rot 1)
+equal to gate_up(a_rot 0), gate_up_down equal to its pair, zero rows, prep_gu's unwritten regions, replay determinism.
 """
 import numpy as np
 import pytest
 
-from cases import Case, Dev, bf16, f16, rel_err
+from cases import Case, Dev, bf16, f16, narrowed_ok, rel_err, rel_l2
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
+CHAIN_TOL = 4e-3
 
 
 @pytest.fixture(scope="module")
@@ -69,6 +72,17 @@ def test_dequant_covers_every_mul1_state_at_the_expert_geometry(torch_cuda):
 SMALL = dict(n_tok=4, top_k=4, n_expert=8, geoms=[(256, 128)], bits=4, cb="mul1")
 
 
+def _acc_ok(got, want, case, which):
+    """The north star's bar on the f32 accumulations themselves: max-abs <= 2e-3 x RMS over each live row's own
+    columns (a narrower class's row has fewer)."""
+    g, w = [], []
+    for e, rows in case.live_rows().items():
+        n = (case.gu if which == "gu" else case.dn)[e].rows
+        g.append(got[rows, :n].ravel())
+        w.append(want[rows, :n].ravel())
+    return rel_err(np.concatenate(g), np.concatenate(w)) <= TOL
+
+
 def _check_all(case, label):
     dev = Dev(case)
     _say(f"{label}: prep_gu")
@@ -78,28 +92,35 @@ def _check_all(case, label):
 
     _say(f"{label}: gate_up h_rot 0 / 1, a_rot 0 / 1")
     h0 = dev.gate_up(h_rot=0)
+    N = max(g.rows for g in case.gu)
+    assert _acc_ok(dev.last_acc()[:, :N], case.oracle_gu_acc(xr_o), case, "gu")
     h0_o = case.oracle_gate_up(h_rot=0)
-    assert rel_err(f16(h0), f16(h0_o)) <= TOL
+    assert narrowed_ok(h0, h0_o, "f16") == 0
+    assert rel_l2(f16(h0), f16(h0_o)) <= CHAIN_TOL
     h1 = dev.gate_up(h_rot=1)
-    assert rel_err(f16(h1), f16(case.oracle_gate_up(h_rot=1))) <= TOL
+    assert np.array_equal(h1, case.h_rot_of(h0))        # h_rot = 1 is down's first step on its own h, to the bit
+    assert rel_l2(f16(h1), f16(case.oracle_gate_up(h_rot=1))) <= CHAIN_TOL
     xr_t = dev.torch.from_numpy(xr_d.view(np.int16)).cuda()
     assert np.array_equal(dev.gate_up(h_rot=0, a_rot=1, xr=xr_t), h0)          # prep_gu -> gate_up(a_rot 1): same bits
     assert np.array_equal(dev.gate_up(h_rot=1, a_rot=1, xr=xr_t), h1)
 
     _say(f"{label}: down h_rot 0 / 1, gate_up_down")
-    y0 = dev.down(h0, h_rot=0)
-    y0_o = case.oracle_down(h0, h_rot=0)               # the oracle's down on the DEVICE's h: isolates down
-    assert rel_err(bf16(y0), bf16(y0_o)) <= TOL
+    y0 = dev.down(h0, h_rot=0)                         # the oracle's down on the DEVICE's h: isolates down
+    Nd = max(d.rows for d in case.dn)
+    assert _acc_ok(dev.last_acc()[:, :Nd], case.oracle_dn_acc(h0, h_rot=0), case, "dn")
+    y0_o = case.oracle_down(h0, h_rot=0)
+    assert narrowed_ok(y0, y0_o, "bf16") == 0
+    assert rel_l2(bf16(y0), bf16(y0_o)) <= CHAIN_TOL
     y1 = dev.down(h1, h_rot=1)
     assert np.array_equal(y1, y0)                      # the pair's bits do not depend on h_rot
     gd = dev.gate_up_down()
     assert np.array_equal(gd, y1)                      # gate_up_down is its pair, to the bit
-    gd_o = case.oracle_gate_up_down()
-    assert rel_err(bf16(gd), bf16(gd_o)) <= TOL
+    assert rel_l2(bf16(gd), bf16(case.oracle_gate_up_down())) <= CHAIN_TOL
+    assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
 
     # zero rows: dropped slots, rows past the live count (whatever sorted_tok holds there), outside the runs
-    T, live = case.T, int(case.off[-1])
-    dead = np.array([i >= live or i < case.off[0] or case.sorted_tok[i] < 0 for i in range(T)])
+    T, n_live = case.T, int(case.off[-1])
+    dead = np.array([i >= n_live or i < case.off[0] or case.sorted_tok[i] < 0 for i in range(T)])
     for out in (h0, h1, y0, gd):
         assert np.all(out[dead] == 0)
     # determinism: a replay writes the same bytes
@@ -141,4 +162,11 @@ def test_single_routed_expert_at_the_baseline_geometry(torch_cuda, bits, m):
     dev = Dev(case)
     _say(f"single expert K={bits} m={m}")
     gd = dev.gate_up_down()
-    assert rel_err(bf16(gd), bf16(case.oracle_gate_up_down())) <= TOL
+    assert rel_l2(bf16(gd), bf16(case.oracle_gate_up_down())) <= CHAIN_TOL
+    h0 = dev.gate_up(h_rot=0)
+    xr_o = case.oracle_prep()
+    assert _acc_ok(dev.last_acc(), case.oracle_gu_acc(xr_o), case, "gu")
+    assert narrowed_ok(h0, case.oracle_gate_up(h_rot=0), "f16") == 0
+    h1 = dev.gate_up(h_rot=1)
+    assert np.array_equal(h1, case.h_rot_of(h0))
+    assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
