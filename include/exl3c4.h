@@ -107,10 +107,10 @@ int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
  * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
-/* The kernels one launch runs, in order (gate_up_down runs all but a prep_gu op's prep; down runs prep only at
- * h_rot = 0; gate_up runs prep only at a_rot = 0). */
-enum { EXL3C4_K_PLAN = 0, EXL3C4_K_PREP = 1, EXL3C4_K_GEMV_GU = 2, EXL3C4_K_EPI_GU = 3, EXL3C4_K_GEMV_DN = 4,
-       EXL3C4_K_EPI_DN = 5 };
+/* The kernels one launch runs, in order: the front (the chunk plan, the zeroed rows and the input rotation; prep_gu is
+ * the front alone); gate_up's GEMM, then for gate_up alone its epilogue; down's GEMM with its epilogue (in
+ * gate_up_down it also forms h from gate_up's partial sums). */
+enum { EXL3C4_K_FRONT = 0, EXL3C4_K_GEMV_GU = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3 };
 
 /* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and
  * ev_stop (two hipEvent_t the caller created) at its start and end: the duration of that one kernel, read with
@@ -120,7 +120,7 @@ enum { EXL3C4_K_PLAN = 0, EXL3C4_K_PREP = 1, EXL3C4_K_GEMV_GU = 2, EXL3C4_K_EPI_
 int exl3c4_launch_timed(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop);
 
-/* Where a launch of `op` leaves the f32 partial sums of its GEMM (gemm 0: gate_up's, or down's for the down op; 1:
+/* Where a launch of `op` leaves the f32 accumulations of its GEMM (gemm 0: gate_up's, or down's for the down op; 1:
  * gate_up_down's down) in its scratch: acc[row][col] = sum over s < *splits of the f32 at scratch + *offset +
  * 4 * (s * *split_stride + row * *pitch + col), for the live rows. The epilogue adds them in this order. For a checker
  * of the accumulation itself (the values before any narrowing); no counterpart in the reference. */

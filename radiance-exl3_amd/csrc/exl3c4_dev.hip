@@ -83,21 +83,22 @@ __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
     v1 = b * kHadScale;
 }
 
-// The expert owning sorted row i: e with off[e] <= i < off[e + 1], or -1 (include/exl3_abi.h:136-141). The offsets
-// are device data nothing checked: a malformed table gives a wrong owner, never a read outside off[0 .. n_expert].
-__device__ __forceinline__ int owner_of(const int32_t* off, int n_expert, int i) {
-    if (i < off[0] || i >= off[n_expert]) return -1;
-    int lo = 0, hi = n_expert;
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (off[mid] <= i) lo = mid;
-        else hi = mid;
-    }
-    return lo;
+// The expert owning sorted row i -- e with off[e] <= i < off[e + 1], or -1 (include/exl3_abi.h:136-141) -- found
+// by a whole wave at once: the number of e in [1, n_expert] with off[e] <= i, counted over
+// one round of independent loads and a wave reduction, checked against off[e] <= i < off[e + 1] (-1 otherwise). A
+// dependent binary search costs one memory latency per halving; this costs about one in all.
+__device__ __forceinline__ int owner_wave(const int32_t* off, int n_expert, int i, int lane) {
+    int cnt = 0;
+#pragma unroll 8
+    for (int e = 1 + lane; e <= n_expert; e += 64) cnt += off[e] <= i ? 1 : 0;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
+    const int e = min(cnt, n_expert - 1);
+    return (off[e] <= i && i < off[e + 1]) ? e : -1;
 }
 
-__device__ __forceinline__ int dead_row(const Exl3c4Launch& a, int i, int* owner) {
-    const int e = owner_of(a.off, a.n_expert, i);
+__device__ __forceinline__ int dead_row(const Exl3c4Launch& a, int i, int lane, int* owner) {
+    const int e = owner_wave(a.off, a.n_expert, i, lane);
     *owner = e;
     return e < 0 || a.sorted[i] < 0;
 }
@@ -121,27 +122,35 @@ __device__ __forceinline__ Mul1Consts mul1_consts() {
     return k;
 }
 
-// h = x * 0x83DCD12D mod 2^32 for the state in half H of r: (x * 0x83DC mod 2^16) << 16 + x * 0xD12D.
-template <int H> __device__ __forceinline__ uint32_t mul1_hash(uint32_t r, const Mul1Consts& k);
-template <> __device__ __forceinline__ uint32_t mul1_hash<0>(uint32_t r, const Mul1Consts& k) {
-    uint32_t y, h;
-    asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[0,0] op_sel_hi:[0,1]" : "=v"(y) : "v"(r), "s"(k.kh));
-    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[0,0,0,0]" : "=v"(h) : "v"(r), "s"(k.cl), "v"(y));
-    return h;
-}
-template <> __device__ __forceinline__ uint32_t mul1_hash<1>(uint32_t r, const Mul1Consts& k) {
-    uint32_t y, h;
-    asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[1,0] op_sel_hi:[1,1]" : "=v"(y) : "v"(r), "s"(k.kh));
-    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(h) : "v"(r), "s"(k.cl), "v"(y));
-    return h;
-}
+// Two states (in half HA of ra and half HB of rb) -> their two fp16 weights in one dword, low half from ra's. Per
+// state: h = x * 0x83DCD12D mod 2^32 = (x * 0x83DC mod 2^16) << 16 + x * 0xD12D -- v_pk_mul_lo_u16 puts the high
+// partial product in the high half over a zero low half (op_sel), v_mad_u32_u16 adds x * 0xD12D reading only the
+// state's half (op_sel), so no state is masked. Then v_sad_u8 / v_sad_hi_u8 leave 0x6400 + bytesum in each half
+// (fp16 1024 + s, exact), and one v_pk_fma_f16 forms (1024 + s) * K_INV + K_BIAS for both, one rounding each. One asm
+// block a pair, so the compiler pads after it once rather than after every instruction.
+#define EXL3C4_MUL1_PAIR(HA, HB)                                                                            \
+    "v_pk_mul_lo_u16 %[ya], %[ra], %[kh] op_sel:[" #HA ",0] op_sel_hi:[" #HA ",1]\n\t"                    \
+    "v_pk_mul_lo_u16 %[yb], %[rb], %[kh] op_sel:[" #HB ",0] op_sel_hi:[" #HB ",1]\n\t"                    \
+    "v_mad_u32_u16 %[ya], %[ra], %[cl], %[ya] op_sel:[" #HA ",0,0,0]\n\t"                                 \
+    "v_mad_u32_u16 %[yb], %[rb], %[cl], %[yb] op_sel:[" #HB ",0,0,0]\n\t"                                 \
+    "v_sad_u8 %[ya], %[ya], 0, %[c64]\n\t"                                                                \
+    "v_sad_hi_u8 %[ya], %[yb], 0, %[ya]\n\t"                                                              \
+    "v_pk_fma_f16 %[out], %[ya], %[kinv], %[kbias]"
 
-// Two hashes -> two fp16 weights in one dword: low half from ha, high half from hb.
-__device__ __forceinline__ uint32_t mul1_finish(uint32_t ha, uint32_t hb, const Mul1Consts& k) {
-    uint32_t s = __builtin_amdgcn_sad_u8(ha, 0u, k.c6464);   // 0x6400 + bytesum(ha) | 0x6400 << 16
-    s = __builtin_amdgcn_sad_hi_u8(hb, 0u, s);                // + bytesum(hb) << 16
-    const half2_t v = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, s), k.kinv, k.kbias);
-    return __builtin_bit_cast(uint32_t, v);
+template <int HA, int HB>
+__device__ __forceinline__ uint32_t mul1_pair(uint32_t ra, uint32_t rb, const Mul1Consts& k) {
+    uint32_t ya, yb, out;
+    const uint32_t kinv = __builtin_bit_cast(uint32_t, k.kinv), kbias = __builtin_bit_cast(uint32_t, k.kbias);
+#define EXL3C4_ARGS                                                                                          \
+    : [ya] "=&v"(ya), [yb] "=&v"(yb), [out] "=v"(out)                                                       \
+    : [ra] "v"(ra), [rb] "v"(rb), [kh] "s"(k.kh), [cl] "s"(k.cl), [c64] "s"(k.c6464), [kinv] "s"(kinv),    \
+      [kbias] "v"(kbias)
+    if constexpr (HA == 0 && HB == 0) asm(EXL3C4_MUL1_PAIR(0, 0) EXL3C4_ARGS);
+    else if constexpr (HA == 0 && HB == 1) asm(EXL3C4_MUL1_PAIR(0, 1) EXL3C4_ARGS);
+    else if constexpr (HA == 1 && HB == 0) asm(EXL3C4_MUL1_PAIR(1, 0) EXL3C4_ARGS);
+    else asm(EXL3C4_MUL1_PAIR(1, 1) EXL3C4_ARGS);
+#undef EXL3C4_ARGS
+    return out;
 }
 
 // mcg / 3inst (common/exl3_decode.c:59-66): a 32-bit hash, (h & 0x8FFF8FFF) ^ 0x3B603B60, fp16 lo + hi rounded once.
@@ -173,7 +182,7 @@ __device__ __forceinline__ void decode_pair(const uint32_t (&v)[BITS + 1], uint3
     constexpr int ha = state_half<BITS, Q>(), hb = state_half<BITS, Q + 1>();
     uint32_t out;
     if constexpr (CB == EXL3C4_CB_MUL1) {
-        out = mul1_finish(mul1_hash<ha>(ra, k), mul1_hash<hb>(rb, k), k);
+        out = mul1_pair<ha, hb>(ra, rb, k);
     } else {
         out = (uint32_t)lop_value<CB, ha>(ra) | ((uint32_t)lop_value<CB, hb>(rb) << 16);
     }
@@ -200,18 +209,21 @@ __device__ __forceinline__ void decode_segment(const uint32_t (&d)[BITS], uint32
 }
 
 // A lane's K words of one block: K u32 at p (4-byte aligned).
-template <int BITS> __device__ __forceinline__ void load_words(const uint32_t* p, uint32_t (&d)[BITS]) {
+template <int BITS, typename P> __device__ __forceinline__ void load_words(P p, uint32_t (&d)[BITS]) {
+    typedef __attribute__((address_space(1))) const u32x4a_t* q4p;
+    typedef __attribute__((address_space(1))) const u32x3a_t* q3p;
+    typedef __attribute__((address_space(1))) const u32x2a_t* q2p;
     int w = 0;
 #pragma unroll
     for (; w + 4 <= BITS; w += 4) {
-        const u32x4a_t q = *(const u32x4a_t*)(p + w);
+        const u32x4a_t q = *(q4p)(p + w);
         d[w] = q.x; d[w + 1] = q.y; d[w + 2] = q.z; d[w + 3] = q.w;
     }
     if constexpr (BITS % 4 == 3) {
-        const u32x3a_t q = *(const u32x3a_t*)(p + w);
+        const u32x3a_t q = *(q3p)(p + w);
         d[w] = q.x; d[w + 1] = q.y; d[w + 2] = q.z;
     } else if constexpr (BITS % 4 == 2) {
-        const u32x2a_t q = *(const u32x2a_t*)(p + w);
+        const u32x2a_t q = *(q2p)(p + w);
         d[w] = q.x; d[w + 1] = q.y;
     } else if constexpr (BITS % 4 == 1) {
         d[w] = p[w];
@@ -224,12 +236,22 @@ __device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, 
 
 // ------------------------------------------------------------------------------------------------ kernels
 
+// The order of k inside every 16-group of an activation row stored PERMUTED: position p holds k = kPerm[p], so that one
+// 16-byte load is the A operand of the first two MFMAs of a step (k 0,1,8,9,2,3,10,11) and the next 16 bytes the
+// second two (4,5,12,13,6,7,14,15) -- the trellis segment's run pattern. kSlot is its inverse (where k is stored).
+__device__ __forceinline__ int perm_slot(int k) {
+    const int q = k & 15;
+    const int slot = ((q & 1) | ((q >> 3) << 1)) + (((q >> 1) & 1) << 2) + (((q >> 2) & 1) << 3);
+    return (k & ~15) | slot;
+}
+
 // The live chunks: every expert's run clamped to [0, T), cut into row blocks of at most 16, in expert order
-// (the kernels clamp every run, kernels/exl3r4d/launch.c:14-15). One workgroup.
-__global__ __launch_bounds__(256) void k_plan(const Exl3c4Launch a) {
+// (the kernels clamp every run, kernels/exl3r4d/launch.c:14-15). One workgroup; also zeroes the GEMMs' counters.
+__device__ void plan_block(const Exl3c4Launch& a) {
     __shared__ int scan[256];
     __shared__ int carry_s;
     const int tid = threadIdx.x;
+    for (int q = tid; q < a.ctr_n; q += 256) a.ctr[q] = 0;
     if (tid == 0) carry_s = 0;
     __syncthreads();
     int4* ent = (int4*)(a.plan + 4);
@@ -265,55 +287,136 @@ __global__ __launch_bounds__(256) void k_plan(const Exl3c4Launch a) {
     if (tid == 0) a.plan[0] = min(carry_s, a.max_chunks);
 }
 
-// prep: one wave per (sorted row i, half m). Rows outside every run are not written (include/exl3_abi.h:273-278);
-// a run's row whose sorted_tok is negative is written zero.
-__global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a, int halves) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t i = wid / halves;
-    const int m = (int)(wid % halves);
-    if (i >= a.T) return;
-    const int e = owner_of(a.off, a.n_expert, (int)i);
+// Zero one 128-column block of output row i when no GEMM epilogue writes it: a dead row (outside the runs, or
+// sorted_tok < 0: include/exl3_abi.h:125-134) or a narrower class's tail.
+__device__ void zero_block(const Exl3c4Launch& a, int64_t i, int b, int lane) {
+    int e;
+    const int dead = dead_row(a, (int)i, lane, &e);
+    if (!dead && b * 128 < a.z_width[e % a.n_class]) return;
+    uint16_t* out = (uint16_t*)a.z + i * a.z_pitch + b * 128;
+    out[lane] = 0;
+    out[lane + 64] = 0;
+}
+
+// One (sorted row i, half m, 128-block b) of the input rotation xr = f16(had(f16(x * s))). Rows outside every run
+// are not written (include/exl3_abi.h:273-278); a run's row whose sorted_tok is negative is written zero.
+__device__ void prep_block(const Exl3c4Launch& a, int64_t i, int m, int b, int lane) {
+    const int e = owner_wave(a.off, a.n_expert, (int)i, lane);
     if (e < 0) return;
     const int c = e % a.n_class;
     const int64_t jx = e / a.n_class;
     const Exl3c4Class& K = a.cls[c];
     const int C = K.cols;
+    if (b * 128 >= C) return;
     const uint16_t* s = (const uint16_t*)(m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx));
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C;
+    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C + b * 128;
+    const int k0 = a.prep_perm ? perm_slot(lane) : lane, k1 = k0 + 64;
     const int tok = a.sorted[i];
     if (tok < 0) {
-        for (int k = lane; k < C; k += 64) out[k] = 0;
+        out[k0] = 0;
+        out[k1] = 0;
         return;
     }
     int64_t src = a.prep_mode == EXL3C4_PREP_DN ? i : tok / a.top_k;
     src = src < a.x_rows ? src : a.x_rows - 1;
-    const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch;
-    for (int b = 0; b < C; b += 128) {
-        const uint16_t x0 = x[b + lane], x1 = x[b + 64 + lane];
-        const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
-        const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
-        float v0 = h2f(f2h(f0 * h2f(s[b + lane])));
-        float v1 = h2f(f2h(f1 * h2f(s[b + 64 + lane])));
-        had128_wave(v0, v1, lane);
-        out[b + lane] = f2h(v0);
-        out[b + 64 + lane] = f2h(v1);
-    }
+    const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch + b * 128;
+    const uint16_t x0 = x[lane], x1 = x[64 + lane];
+    const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
+    const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
+    float v0 = h2f(f2h(f0 * h2f(s[b * 128 + lane])));
+    float v1 = h2f(f2h(f1 * h2f(s[b * 128 + 64 + lane])));
+    had128_wave(v0, v1, lane);
+    out[k0] = f2h(v0);
+    out[k1] = f2h(v1);
 }
 
-// gemv: one wave per unit (chunk, 32-column strip, k split). Partial sums of the strip for the chunk's rows go to
-// part[split][row][col]; the epilogue adds the splits in a fixed order, so the bits do not depend on scheduling.
-template <int BITS, int CB>
+// The front of a launch: workgroup 0 plans the chunks and zeroes the counters; then one wave per 128-block of the
+// output rows no epilogue will write (zeroed), then one wave per (row, half, 128-block) of the input rotation.
+__global__ __launch_bounds__(256) void k_front(const Exl3c4Launch a) {
+    if (blockIdx.x == 0) {
+        if (a.do_plan) plan_block(a);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    int64_t wid = (int64_t)(blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
+    const int zb = a.z_cols / 128;
+    if (wid < a.zero_waves) {
+        zero_block(a, wid / zb, (int)(wid % zb), lane);
+        return;
+    }
+    wid -= a.zero_waves;
+    const int nb = a.x_cols_max / 128;
+    if (wid >= (int64_t)a.T * a.prep_halves * nb) return;
+    const int b = (int)(wid % nb);
+    const int64_t im = wid / nb;
+    prep_block(a, im / a.prep_halves, (int)(im % a.prep_halves), b, lane);
+}
+
+__device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+
+__device__ __forceinline__ float sum_splits(const Exl3c4Launch& a, int64_t i, int col) {
+    const float* p = a.part + i * a.part_pitch + col;
+    float s = p[0];
+    for (int q = 1; q < a.ksplit; ++q) s = s + p[(int64_t)q * a.part_split];
+    return s;
+}
+
+// gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
+// sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
+// values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
+// 187-212).
+__device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
+                                              int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
+    const uint16_t* svh = (const uint16_t*)tab_entry(K.svh, K.svh_stride, jx);
+    const int n0 = b * 128 + lane, n1 = n0 + 64;
+    const int width = K.rows / 2;
+    float g0 = sum_splits(a, i, n0), g1 = sum_splits(a, i, n1);
+    float u0 = sum_splits(a, i, width + n0), u1 = sum_splits(a, i, width + n1);
+    had128_wave(g0, g1, lane);
+    had128_wave(u0, u1, lane);
+    g0 = g0 * h2f(svh[n0]);
+    g1 = g1 * h2f(svh[n1]);
+    u0 = u0 * h2f(svh[width + n0]);
+    u1 = u1 * h2f(svh[width + n1]);
+    const uint16_t h0 = f2h(silu(g0) * u0), h1 = f2h(silu(g1) * u1);
+    if (!h_rot) {
+        v0 = h0;
+        v1 = h1;
+        return;
+    }
+    const uint16_t* ds = (const uint16_t*)tab_entry(K.dn_suh, K.dn_suh_stride, jx);
+    float r0 = h2f(f2h(h2f(h0) * h2f(ds[n0]))), r1 = h2f(f2h(h2f(h1) * h2f(ds[n1])));
+    had128_wave(r0, r1, lane);
+    v0 = f2h(r0);
+    v1 = f2h(r1);
+}
+
+// The epilogue of one 128-column block b of gate_up's output row i (class c, entry jx).
+__device__ void epilogue_row(const Exl3c4Launch& a, int64_t i, int b, int c, int64_t jx, int lane) {
+    uint16_t v0, v1;
+    gate_up_block(a, a.cls[c], i, b, jx, a.h_rot, lane, v0, v1);
+    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
+    const int o0 = a.out_perm ? perm_slot(lane) : lane;
+    out[o0] = v0;
+    out[o0 + 64] = v1;
+}
+
+// gemv: one wave per unit (chunk, 32-column strip, k split). The unit's partial sums of its strip for the chunk's
+// rows go to part[split][row][col]; the epilogue adds the splits in a fixed order, so the bits do not depend on
+// scheduling. PERM: the activation rows are stored permuted (perm_slot), so each A operand is one 16-byte load.
+typedef const uint32_t __attribute__((address_space(1)))* gu32p;
+typedef const uint16_t __attribute__((address_space(1)))* gu16p;
+
+template <int BITS, int CB, bool PERM>
 __global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
-    const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int S = a.ksplit;
-    const int split = (int)(unit % S);
-    const int64_t t = unit / S;
-    const int strip = (int)(t % a.max_strips);
-    const int64_t chunk = t / a.max_strips;
+    // grid: y = chunk, x * 4 + wave = strip * S + split (S a power of two)
+    const int chunk = blockIdx.y;
     const int nch = min(a.plan[0], a.max_chunks);
     if (chunk >= nch) return;
+    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int S = a.ksplit;
+    const int strip = u >> a.ksplit_log2, split = u & (S - 1);
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
     const int c = e % a.n_class;
@@ -325,32 +428,50 @@ __global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
     const int per = (ksteps + S - 1) / S;
     const int ks0 = split * per, ks1 = min(ksteps, ks0 + per);
 
-    const uint32_t* rec = (const uint32_t*)tab_entry(K.codes, K.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS;
+    const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    // A: the row of this lane's token; a lane past the chunk's rows reads a clamped row whose products land only in
+    // output rows that are never stored
     const int r = lane & 15, g = lane >> 4;
-    const int i = row0 + r;
-    bool valid = r < nrows;
-    if (valid) valid = a.sorted[i] >= 0;
-    const int acol = (a.gate_up && strip * EXL3C4_STRIP >= N / 2) ? KC : 0;
-    const uint16_t* arow = (const uint16_t*)a.a + (int64_t)(valid ? i : 0) * a.a_pitch + acol + 16 * g;
+    const int i = min(row0 + r, a.T - 1);
+    const bool up = a.gate_up && strip * EXL3C4_STRIP >= N / 2;
+    const gu16p arow = (gu16p)a.a + (int64_t)i * a.a_pitch + (up ? KC : 0) + 16 * g;
 
     const Mul1Consts k = mul1_consts();
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    for (int ks = ks0; ks < ks1; ++ks) {
-        uint32_t d[BITS];
-        load_words<BITS>(rec + ((int64_t)ks * 64 + lane) * BITS, d);
-        u32x4_t c0 = { 0, 0, 0, 0 }, c1 = { 0, 0, 0, 0 };
-        if (valid) {
-            c0 = *(const u32x4_t*)(arow + ks * EXL3C4_KSTEP);
-            c1 = *(const u32x4_t*)(arow + ks * EXL3C4_KSTEP + 8);
-        }
+    auto load_step = [&](int ks, uint32_t (&d)[BITS], u32x4_t& c0, u32x4_t& c1) {
+        load_words<BITS>(rec + ks * 64 * BITS, d);
+        c0 = *(const __attribute__((address_space(1))) u32x4_t*)(arow + ks * EXL3C4_KSTEP);
+        c1 = *(const __attribute__((address_space(1))) u32x4_t*)(arow + ks * EXL3C4_KSTEP + 8);
+    };
+    auto mma_step = [&](const uint32_t (&d)[BITS], const u32x4_t& c0, const u32x4_t& c1) {
         uint32_t B[16];
         decode_segment<BITS, CB>(d, B, k);
-        const half8_t Aa = as_half8(c0.x, c1.x, c0.y, c1.y), Ab = as_half8(c0.z, c1.z, c0.w, c1.w);
+        half8_t Aa, Ab;
+        if constexpr (PERM) {
+            Aa = __builtin_bit_cast(half8_t, c0);
+            Ab = __builtin_bit_cast(half8_t, c1);
+        } else {
+            Aa = as_half8(c0.x, c1.x, c0.y, c1.y);
+            Ab = as_half8(c0.z, c1.z, c0.w, c1.w);
+        }
         acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
+    };
+    // two steps in flight: the next step's loads are issued before this step's decode
+    uint32_t dA[BITS], dB[BITS];
+    u32x4_t a0, a1, b0, b1;
+    int ks = ks0;
+    if (ks < ks1) load_step(ks, dA, a0, a1);
+    for (; ks + 1 < ks1; ks += 2) {
+        load_step(ks + 1, dB, b0, b1);
+        mma_step(dA, a0, a1);
+        if (ks + 2 < ks1) load_step(ks + 2, dA, a0, a1);
+        mma_step(dB, b0, b1);
     }
+    if (ks < ks1) mma_step(dA, a0, a1);
+
     // D lane l: column l % 16 (c' = 2 s + t -> weight row 32 nb + 16 t + s, + 8 for acc1), rows 4 (l / 16) + 0..3
     const int cc = lane & 15, rg = lane >> 4;
     const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
@@ -363,69 +484,127 @@ __global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
             pp[(int64_t)(row0 + tok) * a.part_pitch + n + 8] = acc1[q];
         }
     }
+
 }
 
-__device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
-
-__device__ __forceinline__ float sum_splits(const Exl3c4Launch& a, int64_t i, int col) {
-    const float* p = a.part + i * a.part_pitch + col;
-    float s = p[0];
-    for (int q = 1; q < a.ksplit; ++q) s = s + p[(int64_t)q * a.part_split];
-    return s;
-}
-
-// epilogue: one wave per (row i, 128-column block b of the output). Dead rows and a narrower class's tail are zero.
+// epilogue: one wave per (chunk, 128-column output block b): the chunk's live rows of that block, from the partial
+// sums of the GEMM that ran before it (the kernel boundary orders and publishes them). Dead rows and a narrower class's
+// tail were zeroed by the front.
 __global__ __launch_bounds__(256) void k_epilogue(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
-    const int nblk = a.y_cols / 128;
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int64_t i = wid / nblk;
-    const int b = (int)(wid % nblk);
-    if (i >= a.T) return;
-    int e;
-    const int dead = dead_row(a, (int)i, &e);
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
-    int width = 0, c = 0;
-    int64_t jx = 0;
-    if (!dead) {
-        c = e % a.n_class;
-        jx = e / a.n_class;
-        width = a.gate_up ? a.cls[c].rows / 2 : a.cls[c].rows;
+    const int b = (int)(wid % a.nblk);
+    const int64_t chunk = wid / a.nblk;
+    const int nch = min(a.plan[0], a.max_chunks);
+    if (chunk >= nch) return;
+    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
+    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const int c = e % a.n_class;
+    if (b * 128 >= a.cls[c].rows / 2) return;
+    for (int q = 0; q < nrows; ++q) {
+        if (a.sorted[row0 + q] < 0) continue;
+        epilogue_row(a, row0 + q, b, c, e / a.n_class, lane);
     }
-    if (dead || b * 128 >= width) {
-        out[lane] = 0;
-        out[lane + 64] = 0;
-        return;
-    }
-    const Exl3c4Class& K = a.cls[c];
-    const uint16_t* svh = (const uint16_t*)tab_entry(K.svh, K.svh_stride, jx);
-    const int n0 = b * 128 + lane, n1 = n0 + 64;
-    if (a.gate_up) {
-        float g0 = sum_splits(a, i, n0), g1 = sum_splits(a, i, n1);
-        float u0 = sum_splits(a, i, width + n0), u1 = sum_splits(a, i, width + n1);
-        had128_wave(g0, g1, lane);
-        had128_wave(u0, u1, lane);
-        g0 = g0 * h2f(svh[n0]);
-        g1 = g1 * h2f(svh[n1]);
-        u0 = u0 * h2f(svh[width + n0]);
-        u1 = u1 * h2f(svh[width + n1]);
-        const uint16_t h0 = f2h(silu(g0) * u0), h1 = f2h(silu(g1) * u1);
-        if (!a.h_rot) {
-            out[lane] = h0;
-            out[lane + 64] = h1;
-            return;
+}
+
+// down, one workgroup per (chunk, 128-column output block b): its four waves take the block's four 32-column strips
+// over all of k, so the block's output is whole inside the workgroup and its epilogue (had128, x svh, bf16) runs
+// there. The chunk's input rows are staged in LDS first (permuted, so each A operand is one ds_read_b128): gate_up's
+// h_rot = 1 output computed here from gate_up's partial sums (gate_up_down), or the rows of `a` (down alone). The
+// raw accumulations also go to `dacc` (a checker's view of the sums before any narrowing).
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) void k_dn(const Exl3c4Launch a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int b = blockIdx.x, chunk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = min(a.plan[0], a.max_chunks);
+    if (chunk >= nch) return;
+    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
+    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const int c = e % a.n_class;
+    const int64_t jx = e / a.n_class;
+    const Exl3c4Class& D = a.cls[c];
+    const int N = D.rows, KC = D.cols;
+    if (b * 128 >= N) return;
+    const int kp = a.lds_pitch;                                   // halves a staged row
+    uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
+    float* acc_l = (float*)(lds + 16 * kp * 2);                   // [16][128]
+
+    // stage the chunk's rows
+    const int nhb = KC / 128;
+    for (int t = wave; t < nrows * nhb; t += 4) {
+        const int q = t / nhb, hb = t % nhb;
+        const int64_t i = row0 + q;
+        uint16_t v0, v1;
+        if (a.h_from_gu) {
+            if (a.sorted[i] < 0) continue;                         // its outputs are never stored
+            gate_up_block(a, a.gcls[c], i, hb, jx, 1, lane, v0, v1);
+            const int o = perm_slot(lane);
+            A[q * kp + hb * 128 + o] = v0;
+            A[q * kp + hb * 128 + o + 64] = v1;
+        } else {
+            const uint16_t* src = (const uint16_t*)a.a + i * a.a_pitch + hb * 128;
+            const int o = a.a_perm ? lane : perm_slot(lane);    // scratch rows are already permuted
+            A[q * kp + hb * 128 + o] = src[lane];
+            A[q * kp + hb * 128 + o + 64] = src[lane + 64];
         }
-        // h_rot = 1: down's first step, with down's suh of this expert (docs/OPS-exl3.md:120-123)
-        const uint16_t* ds = (const uint16_t*)tab_entry(K.dn_suh, K.dn_suh_stride, jx);
-        float v0 = h2f(f2h(h2f(h0) * h2f(ds[n0]))), v1 = h2f(f2h(h2f(h1) * h2f(ds[n1])));
-        had128_wave(v0, v1, lane);
-        out[lane] = f2h(v0);
-        out[lane + 64] = f2h(v1);
-    } else {
-        float y0 = sum_splits(a, i, n0), y1 = sum_splits(a, i, n1);
+    }
+    __syncthreads();
+
+    // this wave's strip of the block, all of k
+    const int strip = 4 * b + wave;
+    const int ksteps = KC / EXL3C4_KSTEP;
+    const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    const int r = lane & 15, g = lane >> 4;
+    const uint16_t* arow = A + r * kp + 16 * g;
+    const Mul1Consts k = mul1_consts();
+    float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
+    auto mma_step = [&](const uint32_t (&d)[BITS], int ks) {
+        uint32_t B[16];
+        decode_segment<BITS, CB>(d, B, k);
+        const half8_t Aa = *(const half8_t*)(arow + ks * EXL3C4_KSTEP);
+        const half8_t Ab = *(const half8_t*)(arow + ks * EXL3C4_KSTEP + 8);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
+    };
+    uint32_t dA[BITS], dB[BITS];
+    int ks = 0;
+    if (ks < ksteps) load_words<BITS>(rec, dA);
+    for (; ks + 1 < ksteps; ks += 2) {
+        load_words<BITS>(rec + (ks + 1) * 64 * BITS, dB);
+        mma_step(dA, ks);
+        if (ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dA);
+        mma_step(dB, ks + 1);
+    }
+    if (ks < ksteps) mma_step(dA, ks);
+
+    // the block's accumulations to LDS (column of D lane l: 16 (l & 1) + (l / 2) within the strip, + 8 for acc1)
+    const int cc = lane & 15, rg = lane >> 4;
+    const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int tok = rg * 4 + q;
+        if (tok < nrows) {
+            acc_l[tok * 128 + col] = acc0[q];
+            acc_l[tok * 128 + col + 8] = acc1[q];
+        }
+    }
+    __syncthreads();
+
+    const uint16_t* svh = (const uint16_t*)tab_entry(D.svh, D.svh_stride, jx);
+    for (int q = wave; q < nrows; q += 4) {
+        const int64_t i = row0 + q;
+        float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
+        float* dacc = a.dacc + i * a.dacc_pitch + b * 128;
+        dacc[lane] = y0;
+        dacc[lane + 64] = y1;
+        if (a.sorted[i] < 0) continue;                             // zeroed by the front
         had128_wave(y0, y1, lane);
-        out[lane] = f2bf(y0 * h2f(svh[n0]));
-        out[lane + 64] = f2bf(y1 * h2f(svh[n1]));
+        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
+        out[lane] = f2bf(y0 * h2f(svh[b * 128 + lane]));
+        out[lane + 64] = f2bf(y1 * h2f(svh[b * 128 + 64 + lane]));
     }
 }
 
@@ -438,7 +617,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* rec, int rows, 
     if (blk >= (int64_t)ksteps * strips) return;
     const int strip = (int)(blk / ksteps), ks = (int)(blk % ksteps);
     uint32_t d[BITS];
-    load_words<BITS>(rec + (blk * 64 + lane) * BITS, d);
+    load_words<BITS>((const __attribute__((address_space(1))) uint32_t*)rec + (blk * 64 + lane) * BITS, d);
     uint32_t B[16];
     decode_segment<BITS, CB>(d, B, mul1_consts());
     const int cc = lane & 15, g = lane >> 4;
@@ -460,13 +639,14 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* rec, int rows, 
 typedef void (*GemvFn)(const Exl3c4Launch);
 typedef void (*DequantFn)(const uint32_t*, int, int, uint16_t*, int64_t);
 
-template <int BITS> GemvFn gemv_fn(int cb) {
+template <int BITS, bool PERM> GemvFn gemv_fn2(int cb) {
     switch (cb) {
-    case EXL3C4_CB_MUL1: return k_gemv<BITS, EXL3C4_CB_MUL1>;
-    case EXL3C4_CB_MCG:  return k_gemv<BITS, EXL3C4_CB_MCG>;
-    default:             return k_gemv<BITS, EXL3C4_CB_3INST>;
+    case EXL3C4_CB_MUL1: return k_gemv<BITS, EXL3C4_CB_MUL1, PERM>;
+    case EXL3C4_CB_MCG:  return k_gemv<BITS, EXL3C4_CB_MCG, PERM>;
+    default:             return k_gemv<BITS, EXL3C4_CB_3INST, PERM>;
     }
 }
+template <int BITS> GemvFn gemv_fn(int cb, bool perm) { return perm ? gemv_fn2<BITS, true>(cb) : gemv_fn2<BITS, false>(cb); }
 template <int BITS> DequantFn dequant_fn(int cb) {
     switch (cb) {
     case EXL3C4_CB_MUL1: return k_dequant<BITS, EXL3C4_CB_MUL1>;
@@ -475,15 +655,35 @@ template <int BITS> DequantFn dequant_fn(int cb) {
     }
 }
 
-GemvFn pick_gemv(int bits, int cb) {
+template <int BITS> GemvFn dn_fn(int cb) {
+    switch (cb) {
+    case EXL3C4_CB_MUL1: return k_dn<BITS, EXL3C4_CB_MUL1>;
+    case EXL3C4_CB_MCG:  return k_dn<BITS, EXL3C4_CB_MCG>;
+    default:             return k_dn<BITS, EXL3C4_CB_3INST>;
+    }
+}
+GemvFn pick_dn(int bits, int cb) {
     switch (bits) {
-    case 2: return gemv_fn<2>(cb);
-    case 3: return gemv_fn<3>(cb);
-    case 4: return gemv_fn<4>(cb);
-    case 5: return gemv_fn<5>(cb);
-    case 6: return gemv_fn<6>(cb);
-    case 7: return gemv_fn<7>(cb);
-    case 8: return gemv_fn<8>(cb);
+    case 2: return dn_fn<2>(cb);
+    case 3: return dn_fn<3>(cb);
+    case 4: return dn_fn<4>(cb);
+    case 5: return dn_fn<5>(cb);
+    case 6: return dn_fn<6>(cb);
+    case 7: return dn_fn<7>(cb);
+    case 8: return dn_fn<8>(cb);
+    default: return nullptr;
+    }
+}
+
+GemvFn pick_gemv(int bits, int cb, bool perm) {
+    switch (bits) {
+    case 2: return gemv_fn<2>(cb, perm);
+    case 3: return gemv_fn<3>(cb, perm);
+    case 4: return gemv_fn<4>(cb, perm);
+    case 5: return gemv_fn<5>(cb, perm);
+    case 6: return gemv_fn<6>(cb, perm);
+    case 7: return gemv_fn<7>(cb, perm);
+    case 8: return gemv_fn<8>(cb, perm);
     default: return nullptr;
     }
 }
@@ -515,30 +715,42 @@ int go(F f, unsigned blocks, hipStream_t s, void* ev0, void* ev1, Args... args) 
 
 unsigned blocks_for_waves(int64_t waves) { return (unsigned)((waves + 3) / 4); }
 
+template <typename F, typename... Args>
+int go2(F f, dim3 grid, hipStream_t s, void* ev0, void* ev1, uint32_t lds, Args... args) {
+    if (ev0 && ev1)
+        hipExtLaunchKernelGGL(f, grid, dim3(256), lds, s, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, args...);
+    else
+        hipLaunchKernelGGL(f, grid, dim3(256), lds, s, args...);
+    return hipGetLastError() == hipSuccess ? 0 : EXL3C4_E_DEVICE;
+}
+
 }  // namespace
 
-extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    return go(k_plan, 1, (hipStream_t)stream, ev0, ev1, *a);
-}
-
-extern "C" int exl3c4_dev_prep(const Exl3c4Launch* a, int halves, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->T * halves;
-    if (waves <= 0) return 0;
-    return go(k_prep, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a, halves);
-}
-
-extern "C" int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemvFn f = pick_gemv(a->bits, a->codebook);
-    if (!f) return EXL3C4_E_DTYPE;
-    const int64_t waves = (int64_t)a->max_chunks * a->max_strips * a->ksplit;
-    if (waves <= 0) return 0;
-    return go(f, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+extern "C" int exl3c4_dev_front(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = (int64_t)a->zero_waves + (int64_t)a->T * a->prep_halves * (a->x_cols_max / 128);
+    return go(k_front, 1 + blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 extern "C" int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->T * (a->y_cols / 128);
+    const int64_t waves = (int64_t)a->max_chunks * a->nblk;
     if (waves <= 0) return 0;
     return go(k_epilogue, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+}
+
+extern "C" int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemvFn f = pick_gemv(a->bits, a->codebook, a->a_perm != 0);
+    if (!f) return EXL3C4_E_DTYPE;
+    const int64_t waves = (int64_t)a->max_strips * a->ksplit;
+    if (waves <= 0 || a->max_chunks <= 0) return 0;
+    return go2(f, dim3(blocks_for_waves(waves), a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
+}
+
+extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemvFn f = pick_dn(a->bits, a->codebook);
+    if (!f) return EXL3C4_E_DTYPE;
+    if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
+    const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2 + 16 * 128 * 4);
+    return go2(f, dim3(a->nblk, a->max_chunks), (hipStream_t)stream, ev0, ev1, lds, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

@@ -41,21 +41,30 @@ static int64_t chunk_bound(int64_t T, int64_t n_expert) {
 
 /* Split-K of one GEMV launch, from the geometry alone (never the routing, so a row's bits do not depend on the batch):
  * enough waves to fill the device, at most 16 splits and never more than the k steps. */
+#ifndef EXL3C4_TARGET_WAVES
+#define EXL3C4_TARGET_WAVES 8192
+#endif
 static int ksplit_for(int64_t chunks, int64_t strips, int64_t ksteps) {
     const int64_t units = chunks * strips;
-    int64_t s = units > 0 ? (8192 + units - 1) / units : 1;
-    if (s > 16) s = 16;
-    if (s > ksteps) s = ksteps;
-    return s < 1 ? 1 : (int)s;
+    int s = 1;
+    while (s < 16 && 2 * s <= ksteps && units * s < EXL3C4_TARGET_WAVES) s *= 2;   /* a power of two */
+    return s;
+}
+
+static int log2i(int v) {
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
 }
 
 typedef struct Carve {
-    int64_t plan, xr, part, h, total;
-    int64_t chunks, T, xr_pitch, part_pitch, h_pitch;
-    int     split_gu, split_dn;
+    int64_t plan, ctr, xr, part, dacc, total;
+    int64_t chunks, T, xr_pitch, part_pitch, dacc_pitch, dn_kmax;
+    int     split_gu, nblk_gu;
 } Carve;
 
-/* The scratch of one launch with T sorted rows: [plan | xr | partials | h], each 256-B aligned. */
+/* The scratch of one launch with T sorted rows: [plan | xr | gate_up partial sums | down accumulations], each region
+ * 256-B aligned. */
 static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     const int op = o->op;
     const int64_t xc = max_cols(o), rc = max_rows(o);
@@ -65,40 +74,35 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     int64_t off = 0;
     k->plan = off;
     off += ALIGN_UP(16 + 16 * k->chunks, 256);
+    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) k->nblk_gu = (int)(rc / 2 / 128);
+    k->ctr = off;
     k->xr = off;
     if (op == EXL3C4_GATE_UP && !o->a_rot) k->xr_pitch = 2 * xc;
     else if (op == EXL3C4_GU_DN) k->xr_pitch = 2 * xc;
     else if (op == EXL3C4_DOWN && !o->h_rot) k->xr_pitch = xc;
     off += ALIGN_UP(T * k->xr_pitch * 2, 256);
     k->part = off;
-    int64_t part_cols = 0, part_splits = 1;
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         int64_t kmin = INT64_MAX;
         for (int c = 0; c < o->n_class; ++c)
             if (o->cls[c].cols / EXL3C4_KSTEP < kmin) kmin = o->cls[c].cols / EXL3C4_KSTEP;
         k->split_gu = ksplit_for(k->chunks, rc / EXL3C4_STRIP, kmin);
-        if (rc > part_cols) part_cols = rc;
-        if (k->split_gu > part_splits) part_splits = k->split_gu;
+        k->part_pitch = rc;
+        off += ALIGN_UP(k->split_gu * T * rc * 4, 256);
     }
+    k->dacc = off;
     if (op == EXL3C4_DOWN || op == EXL3C4_GU_DN) {
         /* down's geometry: its own classes, or gate_up_down's [cols, rows / 2] */
-        int64_t kmin = INT64_MAX, nmax = 0;
+        int64_t nmax = 0, kmax = 0;
         for (int c = 0; c < o->n_class; ++c) {
             const int64_t r = op == EXL3C4_DOWN ? o->cls[c].rows : o->cls[c].cols;
             const int64_t kk = op == EXL3C4_DOWN ? o->cls[c].cols : o->cls[c].rows / 2;
-            if (kk / EXL3C4_KSTEP < kmin) kmin = kk / EXL3C4_KSTEP;
             if (r > nmax) nmax = r;
+            if (kk > kmax) kmax = kk;
         }
-        k->split_dn = ksplit_for(k->chunks, nmax / EXL3C4_STRIP, kmin);
-        if (nmax > part_cols) part_cols = nmax;
-        if (k->split_dn > part_splits) part_splits = k->split_dn;
-    }
-    k->part_pitch = part_cols;
-    off += ALIGN_UP(part_splits * T * part_cols * 4, 256);
-    k->h = off;
-    if (op == EXL3C4_GU_DN) {
-        k->h_pitch = rc / 2;
-        off += ALIGN_UP(T * k->h_pitch * 2, 256);
+        k->dacc_pitch = nmax;
+        k->dn_kmax = kmax;
+        off += ALIGN_UP(T * nmax * 4, 256);
     }
     k->total = off;
 }
@@ -144,6 +148,11 @@ static int check(const Exl3c4Op* o) {
             if (d->codes_stride && (d->codes_stride % 4 || (uintptr_t)d->codes % 4)) return EXL3C4_E_ALIGN;
             if (d->svh_stride & 1) return EXL3C4_E_ALIGN;
         }
+    }
+    /* down stages a chunk's 16 input rows in LDS: at most 1536 columns (57 KiB with its accumulations) */
+    for (int c = 0; c < o->n_class; ++c) {
+        const int64_t kdn = op == EXL3C4_DOWN ? o->cls[c].cols : op == EXL3C4_GU_DN ? o->cls[c].rows / 2 : 0;
+        if (kdn > 1536) return EXL3C4_E_UNSUPPORTED;
     }
     /* the input: token rows (f16 or bf16) or sorted rows (f16) */
     const int token_rows = (op == EXL3C4_GATE_UP && !o->a_rot) || op == EXL3C4_PREP_GU || op == EXL3C4_GU_DN;
@@ -196,12 +205,16 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->codebook = o->codebook;
     a->x_dtype = o->x_dtype;
     a->x_rows = (int32_t)o->x_rows;
+    a->x_cols_max = (int32_t)max_cols(o);
 }
 
 /* The events of a timed launch go to exactly one kernel of the sequence. */
 typedef struct Timed { int kernel; void *ev0, *ev1; } Timed;
 #define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
 
+/* Every op is at most three launches on the stream: the front (plan, zero rows, input rotation); gate_up's GEMM
+ * (and, for gate_up alone, its epilogue); down's GEMM, whose workgroups finish their output blocks themselves and, in
+ * gate_up_down, build h from gate_up's partial sums. */
 static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
@@ -212,80 +225,83 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     if (o->T == 0) return EXL3C4_OK;
     char* s = (char*)scratch;
     const int op = o->op;
-    const int64_t xc = max_cols(o), rcw = max_rows(o);
-    Exl3c4Launch a;
-    base_args(o, &k, s, &a);
-    for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
+    const int64_t rcw = max_rows(o);
 
+    /* the front */
+    Exl3c4Launch f;
+    base_args(o, &k, s, &f);
+    for (int c = 0; c < o->n_class; ++c) f.cls[c] = o->cls[c];
+    f.x = o->x;
+    f.x_pitch = o->x_pitch;
     if (op == EXL3C4_PREP_GU) {
-        a.x = o->x; a.x_pitch = o->x_pitch;
-        a.y = o->y; a.y_pitch = o->y_pitch;
-        a.prep_mode = EXL3C4_PREP_GU_OP;
-        return exl3c4_dev_prep(&a, 2, stream, EV(EXL3C4_K_PREP));
+        f.y = o->y; f.y_pitch = o->y_pitch;
+        f.prep_mode = EXL3C4_PREP_GU_OP;
+        f.prep_halves = 2;
+        return exl3c4_dev_front(&f, stream, EV(EXL3C4_K_FRONT));
     }
-    if ((rc = exl3c4_dev_plan(&a, stream, EV(EXL3C4_K_PLAN))) != 0) return rc;
+    f.do_plan = 1;
+    f.z = o->y; f.z_pitch = o->y_pitch; f.z_cols = (int32_t)o->y_cols;
+    f.zero_waves = (int32_t)(o->T * (o->y_cols / 128));
+    for (int c = 0; c < o->n_class; ++c)
+        f.z_width[c] = op == EXL3C4_GATE_UP ? o->cls[c].rows / 2 : op == EXL3C4_GU_DN ? o->cls[c].cols : o->cls[c].rows;
+    const int gu_prep = (op == EXL3C4_GATE_UP && !o->a_rot) || op == EXL3C4_GU_DN;
+    const int dn_prep = op == EXL3C4_DOWN && !o->h_rot;
+    if (gu_prep || dn_prep) {
+        f.y = s + k.xr; f.y_pitch = k.xr_pitch;
+        f.prep_mode = gu_prep ? EXL3C4_PREP_GU_SCRATCH : EXL3C4_PREP_DN;
+        f.prep_halves = gu_prep ? 2 : 1;
+        f.prep_perm = 1;
+    }
+    if ((rc = exl3c4_dev_front(&f, stream, EV(EXL3C4_K_FRONT))) != 0) return rc;
 
+    /* gate_up: its GEMM; alone, its epilogue kernel; in gate_up_down, down stages h from its partial sums */
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
-        if (op == EXL3C4_GU_DN || !o->a_rot) {
-            a.x = o->x; a.x_pitch = o->x_pitch;
-            a.y = s + k.xr; a.y_pitch = k.xr_pitch;
-            a.prep_mode = EXL3C4_PREP_GU_SCRATCH;
-            if ((rc = exl3c4_dev_prep(&a, 2, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
-            a.a = s + k.xr; a.a_pitch = k.xr_pitch;
-        } else {
-            a.a = o->x; a.a_pitch = o->x_pitch;
-        }
+        Exl3c4Launch a;
+        base_args(o, &k, s, &a);
+        for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
+        if (gu_prep) { a.a = s + k.xr; a.a_pitch = k.xr_pitch; a.a_perm = 1; }
+        else { a.a = o->x; a.a_pitch = o->x_pitch; }
         a.gate_up = 1;
         a.ksplit = k.split_gu;
+        a.ksplit_log2 = log2i(k.split_gu);
         a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
+        a.nblk = k.nblk_gu;
+        a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
+        a.h_rot = o->h_rot;
         if ((rc = exl3c4_dev_gemv(&a, stream, EV(EXL3C4_K_GEMV_GU))) != 0) return rc;
-        if (op == EXL3C4_GATE_UP) {
-            a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
-            a.h_rot = o->h_rot;
-            return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU));
-        }
-        a.y = s + k.h; a.y_pitch = k.h_pitch; a.y_cols = (int32_t)k.h_pitch;
-        a.h_rot = 1;
-        if ((rc = exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
-        /* down over h: gate_up_down's down classes [cols, rows / 2], suh = gate_up's dn_suh (include/exl3_abi.h:
-         * 751-800); h crosses rotated (h_rot = 1) */
-        Exl3c4Launch d;
-        base_args(o, &k, s, &d);
-        int64_t nmax = 0;
-        for (int c = 0; c < o->n_class; ++c) {
+        if (op == EXL3C4_GATE_UP) return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU));
+    }
+
+    /* down: its own classes, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
+     * (include/exl3_abi.h:751-800; h crosses rotated), one workgroup per (chunk, 128-column block) */
+    Exl3c4Launch d;
+    base_args(o, &k, s, &d);
+    for (int c = 0; c < o->n_class; ++c) {
+        if (op == EXL3C4_GU_DN) {
             d.cls[c] = o->dn[c];
             d.cls[c].rows = o->cls[c].cols;
             d.cls[c].cols = o->cls[c].rows / 2;
             d.cls[c].suh = o->cls[c].dn_suh;
             d.cls[c].suh_stride = o->cls[c].dn_suh_stride;
-            if (d.cls[c].rows > nmax) nmax = d.cls[c].rows;
+            d.gcls[c] = o->cls[c];
+        } else {
+            d.cls[c] = o->cls[c];
         }
-        d.a = s + k.h; d.a_pitch = k.h_pitch;
-        d.gate_up = 0;
-        d.ksplit = k.split_dn;
-        d.max_strips = (int32_t)(nmax / EXL3C4_STRIP);
-        if ((rc = exl3c4_dev_gemv(&d, stream, EV(EXL3C4_K_GEMV_DN))) != 0) return rc;
-        d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
-        return exl3c4_dev_epilogue(&d, stream, EV(EXL3C4_K_EPI_DN));
     }
-
-    /* down */
-    if (!o->h_rot) {
-        a.x = o->x; a.x_pitch = o->x_pitch;
-        a.y = s + k.xr; a.y_pitch = k.xr_pitch;
-        a.prep_mode = EXL3C4_PREP_DN;
-        if ((rc = exl3c4_dev_prep(&a, 1, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
-        a.a = s + k.xr; a.a_pitch = k.xr_pitch;
+    if (op == EXL3C4_GU_DN) {
+        d.h_from_gu = 1;
+        d.ksplit = k.split_gu;                 /* the gate_up partial sums it reads */
+    } else if (dn_prep) {
+        d.a = s + k.xr; d.a_pitch = k.xr_pitch; d.a_perm = 1;
     } else {
-        a.a = o->x; a.a_pitch = o->x_pitch;
+        d.a = o->x; d.a_pitch = o->x_pitch;
     }
-    (void)xc;
-    a.gate_up = 0;
-    a.ksplit = k.split_dn;
-    a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
-    if ((rc = exl3c4_dev_gemv(&a, stream, EV(EXL3C4_K_GEMV_DN))) != 0) return rc;
-    a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
-    return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_DN));
+    d.nblk = (int32_t)(o->y_cols / 128);
+    d.lds_pitch = (int32_t)k.dn_kmax;
+    d.dacc = (float*)(s + k.dacc);
+    d.dacc_pitch = k.dacc_pitch;
+    d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
+    return exl3c4_dev_dn(&d, stream, EV(EXL3C4_K_DOWN));
 }
 
 int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
@@ -295,7 +311,7 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
 
 int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop) {
-    if (kernel < EXL3C4_K_PLAN || kernel > EXL3C4_K_EPI_DN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
+    if (kernel < EXL3C4_K_FRONT || kernel > EXL3C4_K_DOWN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
     const Timed t = { kernel, ev_start, ev_stop };
     return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }
@@ -308,10 +324,17 @@ int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, in
     if (o->op == EXL3C4_PREP_GU || (gemm == 1 && o->op != EXL3C4_GU_DN) || gemm < 0 || gemm > 1) return EXL3C4_E_INVAL;
     Carve k;
     carve(o, o->T, &k);
-    *offset = k.part;
-    *pitch = k.part_pitch;
-    *split_stride = k.T * k.part_pitch;
-    *splits = (o->op == EXL3C4_DOWN || gemm == 1) ? k.split_dn : k.split_gu;
+    if (o->op == EXL3C4_DOWN || gemm == 1) {
+        *offset = k.dacc;
+        *pitch = k.dacc_pitch;
+        *split_stride = k.T * k.dacc_pitch;
+        *splits = 1;
+    } else {
+        *offset = k.part;
+        *pitch = k.part_pitch;
+        *split_stride = k.T * k.part_pitch;
+        *splits = k.split_gu;
+    }
     return EXL3C4_OK;
 }
 
