@@ -70,14 +70,53 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // The normalised Sylvester Hadamard over one 128-block held by a wave, lane l holding x[l] (v0) and x[l + 64] (v1):
 // the butterfly stages h = 1 .. 64 in the reference's order, each (a + b) low and (a - b) high in f32, then one f32
 // multiply by 1/sqrt(128) (common/exl3_decode.c:172-189) -- the same roundings, so the same bits.
-__device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
-#pragma unroll
-    for (int h = 1; h < 64; h <<= 1) {
-        const float p0 = __shfl_xor(v0, h), p1 = __shfl_xor(v1, h);
-        const bool hi = (lane & h) != 0;
-        v0 = hi ? p0 - v0 : v0 + p0;
-        v1 = hi ? p1 - v1 : v1 + p1;
+// The partners are moved without LDS: DPP for h = 1, 2 (quad_perm), 4 (row_ror 4 or 12), 8 (row_ror 8); gfx950's
+// permlane swaps for 16 and 32, which leave each lane the pair's low-half value and its high-half value.
+template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void bfly(float& v, float p, bool hi) { v = hi ? p - v : v + p; }
+// h = 4: lane l's partner is l - 4 (row_ror 4) when bit 2 of l is set, else l + 4 (row_ror 12). Both moves sit in one
+// asm block so that neither can be sunk under a partial exec mask, where a DPP read of an inactive lane is void.
+__device__ __forceinline__ float partner4(float v, bool hi) {
+    float a, b;
+    asm volatile("s_nop 1\n\tv_mov_b32_dpp %0, %2 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+                 "v_mov_b32_dpp %1, %2 row_ror:12 row_mask:0xf bank_mask:0xf"
+                 : "=&v"(a), "=&v"(b) : "v"(v));
+    return hi ? a : b;
+}
+template <int H> __device__ __forceinline__ void bfly_swap(float& v, bool hi) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    unsigned lo_u, up_u;
+    if constexpr (H == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        lo_u = r[0]; up_u = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        lo_u = r[0]; up_u = r[1];
     }
+    const float lo = __builtin_bit_cast(float, lo_u), up = __builtin_bit_cast(float, up_u);
+    v = hi ? lo - up : lo + up;
+}
+__device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
+    bool hi = lane & 1;
+    bfly(v0, dpp_f<0xB1>(v0), hi);                 // quad_perm [1,0,3,2]
+    bfly(v1, dpp_f<0xB1>(v1), hi);
+    hi = lane & 2;
+    bfly(v0, dpp_f<0x4E>(v0), hi);                 // quad_perm [2,3,0,1]
+    bfly(v1, dpp_f<0x4E>(v1), hi);
+    hi = lane & 4;
+    bfly(v0, partner4(v0, hi), hi);
+    bfly(v1, partner4(v1, hi), hi);
+    hi = lane & 8;
+    bfly(v0, dpp_f<0x128>(v0), hi);
+    bfly(v1, dpp_f<0x128>(v1), hi);
+    hi = lane & 16;
+    bfly_swap<16>(v0, hi);
+    bfly_swap<16>(v1, hi);
+    hi = lane & 32;
+    bfly_swap<32>(v0, hi);
+    bfly_swap<32>(v1, hi);
     const float a = v0 + v1, b = v0 - v1;
     v0 = a * kHadScale;
     v1 = b * kHadScale;
@@ -239,6 +278,10 @@ __device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, 
 // The order of k inside every 16-group of an activation row stored PERMUTED: position p holds k = kPerm[p], so that one
 // 16-byte load is the A operand of the first two MFMAs of a step (k 0,1,8,9,2,3,10,11) and the next 16 bytes the
 // second two (4,5,12,13,6,7,14,15) -- the trellis segment's run pattern. kSlot is its inverse (where k is stored).
+// Expert e's class and its entry in the class's tables: experts interleave over the classes (n_class is 1, 2 or 4).
+__device__ __forceinline__ int class_of(const Exl3c4Launch& a, int e) { return e & (a.n_class - 1); }
+__device__ __forceinline__ int64_t entry_of(const Exl3c4Launch& a, int e) { return e >> (a.n_class >> 1); }
+
 __device__ __forceinline__ int perm_slot(int k) {
     const int q = k & 15;
     const int slot = ((q & 1) | ((q >> 3) << 1)) + (((q >> 1) & 1) << 2) + (((q >> 2) & 1) << 3);
@@ -292,7 +335,7 @@ __device__ void plan_block(const Exl3c4Launch& a) {
 __device__ void zero_block(const Exl3c4Launch& a, int64_t i, int b, int lane) {
     int e;
     const int dead = dead_row(a, (int)i, lane, &e);
-    if (!dead && b * 128 < a.z_width[e % a.n_class]) return;
+    if (!dead && b * 128 < a.z_width[class_of(a, e)]) return;
     uint16_t* out = (uint16_t*)a.z + i * a.z_pitch + b * 128;
     out[lane] = 0;
     out[lane + 64] = 0;
@@ -303,8 +346,8 @@ __device__ void zero_block(const Exl3c4Launch& a, int64_t i, int b, int lane) {
 __device__ void prep_block(const Exl3c4Launch& a, int64_t i, int m, int b, int lane) {
     const int e = owner_wave(a.off, a.n_expert, (int)i, lane);
     if (e < 0) return;
-    const int c = e % a.n_class;
-    const int64_t jx = e / a.n_class;
+    const int c = class_of(a, e);
+    const int64_t jx = entry_of(a, e);
     const Exl3c4Class& K = a.cls[c];
     const int C = K.cols;
     if (b * 128 >= C) return;
@@ -354,11 +397,41 @@ __global__ __launch_bounds__(256) void k_front(const Exl3c4Launch a) {
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
-__device__ __forceinline__ float sum_splits(const Exl3c4Launch& a, int64_t i, int col) {
-    const float* p = a.part + i * a.part_pitch + col;
-    float s = p[0];
-    for (int q = 1; q < a.ksplit; ++q) s = s + p[(int64_t)q * a.part_split];
-    return s;
+// The split-K partial sums of four columns of sorted row i, added in ascending split order (the order fixes the
+// bits). The loads go out four splits at a time (16 registers), so S / 4 round trips in all.
+__device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, const int (&col)[4], float (&out)[4]) {
+    const __attribute__((address_space(1))) float* p =
+        (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
+    const int S = a.ksplit;
+    const int64_t st = a.part_split;
+    if (S < 4) {                                                  // 1 or 2
+        float v[4][2];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            v[c][0] = p[col[c]];
+            v[c][1] = S == 2 ? p[st + col[c]] : 0.f;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) out[c] = S == 2 ? v[c][0] + v[c][1] : v[c][0];
+        return;
+    }
+    for (int q0 = 0; q0 < S; q0 += 4) {
+        float v[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c][q] = p[(int64_t)(q0 + q) * st + col[c]];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float t = q0 == 0 ? v[c][0] : out[c] + v[c][0];
+            t = t + v[c][1];
+            t = t + v[c][2];
+            out[c] = t + v[c][3];
+        }
+    }
+}
+__device__ __forceinline__ uint16_t ldg16(const void* p, int idx) {
+    return ((const __attribute__((address_space(1))) uint16_t*)p)[idx];
 }
 
 // gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
@@ -367,25 +440,29 @@ __device__ __forceinline__ float sum_splits(const Exl3c4Launch& a, int64_t i, in
 // 187-212).
 __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
                                               int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
-    const uint16_t* svh = (const uint16_t*)tab_entry(K.svh, K.svh_stride, jx);
+    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
     const int n0 = b * 128 + lane, n1 = n0 + 64;
     const int width = K.rows / 2;
-    float g0 = sum_splits(a, i, n0), g1 = sum_splits(a, i, n1);
-    float u0 = sum_splits(a, i, width + n0), u1 = sum_splits(a, i, width + n1);
+    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
+    const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
+    const int col[4] = { n0, n1, width + n0, width + n1 };
+    float acc[4];
+    sum_splits4(a, i, col, acc);
+    float g0 = acc[0], g1 = acc[1], u0 = acc[2], u1 = acc[3];
     had128_wave(g0, g1, lane);
     had128_wave(u0, u1, lane);
-    g0 = g0 * h2f(svh[n0]);
-    g1 = g1 * h2f(svh[n1]);
-    u0 = u0 * h2f(svh[width + n0]);
-    u1 = u1 * h2f(svh[width + n1]);
+    g0 = g0 * h2f(sg0);
+    g1 = g1 * h2f(sg1);
+    u0 = u0 * h2f(su0);
+    u1 = u1 * h2f(su1);
     const uint16_t h0 = f2h(silu(g0) * u0), h1 = f2h(silu(g1) * u1);
     if (!h_rot) {
         v0 = h0;
         v1 = h1;
         return;
     }
-    const uint16_t* ds = (const uint16_t*)tab_entry(K.dn_suh, K.dn_suh_stride, jx);
-    float r0 = h2f(f2h(h2f(h0) * h2f(ds[n0]))), r1 = h2f(f2h(h2f(h1) * h2f(ds[n1])));
+    float r0 = h2f(f2h(h2f(h0) * h2f(d0))), r1 = h2f(f2h(h2f(h1) * h2f(d1)));
     had128_wave(r0, r1, lane);
     v0 = f2h(r0);
     v1 = f2h(r1);
@@ -419,8 +496,8 @@ __global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
     const int strip = u >> a.ksplit_log2, split = u & (S - 1);
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
-    const int c = e % a.n_class;
-    const int64_t jx = e / a.n_class;
+    const int c = class_of(a, e);
+    const int64_t jx = entry_of(a, e);
     const Exl3c4Class& K = a.cls[c];
     const int N = K.rows, KC = K.cols;
     if (strip * EXL3C4_STRIP >= N) return;
@@ -499,11 +576,11 @@ __global__ __launch_bounds__(256) void k_epilogue(const Exl3c4Launch a) {
     if (chunk >= nch) return;
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
-    const int c = e % a.n_class;
+    const int c = class_of(a, e);
     if (b * 128 >= a.cls[c].rows / 2) return;
     for (int q = 0; q < nrows; ++q) {
         if (a.sorted[row0 + q] < 0) continue;
-        epilogue_row(a, row0 + q, b, c, e / a.n_class, lane);
+        epilogue_row(a, row0 + q, b, c, entry_of(a, e), lane);
     }
 }
 
@@ -513,7 +590,7 @@ __global__ __launch_bounds__(256) void k_epilogue(const Exl3c4Launch a) {
 // h_rot = 1 output computed here from gate_up's partial sums (gate_up_down), or the rows of `a` (down alone). The
 // raw accumulations also go to `dacc` (a checker's view of the sums before any narrowing).
 template <int BITS, int CB>
-__global__ __launch_bounds__(256) void k_dn(const Exl3c4Launch a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_dn(const Exl3c4Launch a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int b = blockIdx.x, chunk = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -521,40 +598,45 @@ __global__ __launch_bounds__(256) void k_dn(const Exl3c4Launch a) {
     if (chunk >= nch) return;
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
-    const int c = e % a.n_class;
-    const int64_t jx = e / a.n_class;
+    const int c = class_of(a, e);
+    const int64_t jx = entry_of(a, e);
     const Exl3c4Class& D = a.cls[c];
     const int N = D.rows, KC = D.cols;
     if (b * 128 >= N) return;
-    const int kp = a.lds_pitch;                                   // halves a staged row
+    const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
     uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
     float* acc_l = (float*)(lds + 16 * kp * 2);                   // [16][128]
 
+    // this wave's strip of the block, all of k; its first codes are in flight while the rows are staged
+    const int strip = 4 * b + wave;
+    const int ksteps = KC / EXL3C4_KSTEP;
+    const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    uint32_t dA[BITS], dB[BITS];
+    load_words<BITS>(rec, dA);
+    load_words<BITS>(rec + 64 * BITS, dB);                       // k is at least 128: two steps
+
     // stage the chunk's rows
     const int nhb = KC / 128;
-    for (int t = wave; t < nrows * nhb; t += 4) {
-        const int q = t / nhb, hb = t % nhb;
+    for (int q = 0; q < nrows; ++q) {
         const int64_t i = row0 + q;
-        uint16_t v0, v1;
-        if (a.h_from_gu) {
-            if (a.sorted[i] < 0) continue;                         // its outputs are never stored
-            gate_up_block(a, a.gcls[c], i, hb, jx, 1, lane, v0, v1);
-            const int o = perm_slot(lane);
-            A[q * kp + hb * 128 + o] = v0;
-            A[q * kp + hb * 128 + o + 64] = v1;
-        } else {
-            const uint16_t* src = (const uint16_t*)a.a + i * a.a_pitch + hb * 128;
-            const int o = a.a_perm ? lane : perm_slot(lane);    // scratch rows are already permuted
-            A[q * kp + hb * 128 + o] = src[lane];
-            A[q * kp + hb * 128 + o + 64] = src[lane + 64];
+        for (int hb = wave; hb < nhb; hb += 4) {
+            uint16_t v0, v1;
+            if (a.h_from_gu) {
+                if (a.sorted[i] < 0) continue;                     // its outputs are never stored
+                gate_up_block(a, a.gcls[c], i, hb, jx, 1, lane, v0, v1);
+                const int o = perm_slot(lane);
+                A[q * kp + hb * 128 + o] = v0;
+                A[q * kp + hb * 128 + o + 64] = v1;
+            } else {
+                const uint16_t* src = (const uint16_t*)a.a + i * a.a_pitch + hb * 128;
+                const int o = a.a_perm ? lane : perm_slot(lane);    // scratch rows are already permuted
+                A[q * kp + hb * 128 + o] = src[lane];
+                A[q * kp + hb * 128 + o + 64] = src[lane + 64];
+            }
         }
     }
     __syncthreads();
 
-    // this wave's strip of the block, all of k
-    const int strip = 4 * b + wave;
-    const int ksteps = KC / EXL3C4_KSTEP;
-    const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     const int r = lane & 15, g = lane >> 4;
     const uint16_t* arow = A + r * kp + 16 * g;
     const Mul1Consts k = mul1_consts();
@@ -569,14 +651,12 @@ __global__ __launch_bounds__(256) void k_dn(const Exl3c4Launch a) {
         acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
         acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
     };
-    uint32_t dA[BITS], dB[BITS];
     int ks = 0;
-    if (ks < ksteps) load_words<BITS>(rec, dA);
     for (; ks + 1 < ksteps; ks += 2) {
-        load_words<BITS>(rec + (ks + 1) * 64 * BITS, dB);
         mma_step(dA, ks);
         if (ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dA);
         mma_step(dB, ks + 1);
+        if (ks + 3 < ksteps) load_words<BITS>(rec + (ks + 3) * 64 * BITS, dB);
     }
     if (ks < ksteps) mma_step(dA, ks);
 

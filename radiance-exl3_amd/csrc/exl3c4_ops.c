@@ -297,7 +297,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
         d.a = o->x; d.a_pitch = o->x_pitch;
     }
     d.nblk = (int32_t)(o->y_cols / 128);
-    d.lds_pitch = (int32_t)k.dn_kmax;
+    d.lds_pitch = (int32_t)k.dn_kmax + 8;      /* padded: the 16 staged rows start in different LDS banks */
     d.dacc = (float*)(s + k.dacc);
     d.dacc_pitch = k.dacc_pitch;
     d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
