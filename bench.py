@@ -187,7 +187,7 @@ def main():
     evs = [(exl3c4.Event(), exl3c4.Event()) for _ in range(args.steps)]
     for i in range(args.steps):
         a, b = evs[i]
-        rc = exl3c4.launch_timed(ops[i % len(ops)], scratch, exl3c4.K_GEMV_GU, a, b, stream)
+        rc = exl3c4.launch_timed(ops[i % len(ops)], scratch, exl3c4.K_GATE_UP, a, b, stream)
         if rc:
             raise RuntimeError(f"timed launch: {exl3c4.STATUS.get(rc, rc)}")
     torch.cuda.synchronize()

@@ -107,10 +107,9 @@ int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
  * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
-/* The kernels one launch runs, in order: the front (the chunk plan, the zeroed rows and the input rotation; prep_gu is
- * the front alone); gate_up's GEMM, then for gate_up alone its epilogue; down's GEMM with its epilogue (in
- * gate_up_down it also forms h from gate_up's partial sums). */
-enum { EXL3C4_K_FRONT = 0, EXL3C4_K_GEMV_GU = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3 };
+/* The kernels a launch can run: prep_gu's rotation; gate_up's GEMM (with its input rotation), then for gate_up alone
+ * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums). */
+enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3 };
 
 /* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and
  * ev_stop (two hipEvent_t the caller created) at its start and end: the duration of that one kernel, read with

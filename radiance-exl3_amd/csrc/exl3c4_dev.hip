@@ -136,12 +136,6 @@ __device__ __forceinline__ int owner_wave(const int32_t* off, int n_expert, int 
     return (off[e] <= i && i < off[e + 1]) ? e : -1;
 }
 
-__device__ __forceinline__ int dead_row(const Exl3c4Launch& a, int i, int lane, int* owner) {
-    const int e = owner_wave(a.off, a.n_expert, i, lane);
-    *owner = e;
-    return e < 0 || a.sorted[i] < 0;
-}
-
 // ------------------------------------------------------------------------------------------------ the decode
 
 struct Mul1Consts {
@@ -288,62 +282,66 @@ __device__ __forceinline__ int perm_slot(int k) {
     return (k & ~15) | slot;
 }
 
-// The live chunks: every expert's run clamped to [0, T), cut into row blocks of at most 16, in expert order
-// (the kernels clamp every run, kernels/exl3r4d/launch.c:14-15). One workgroup; also zeroes the GEMMs' counters.
-__device__ void plan_block(const Exl3c4Launch& a) {
-    __shared__ int scan[256];
-    __shared__ int carry_s;
-    const int tid = threadIdx.x;
-    for (int q = tid; q < a.ctr_n; q += 256) a.ctr[q] = 0;
-    if (tid == 0) carry_s = 0;
+// The owner of sorted row i and its run, found by a whole workgroup at once: its 256 threads count the experts e in
+// [1, n_expert] with off[e] <= i (one round of independent loads), the counts meet in LDS, and the candidate is
+// checked against off[e] <= i < off[e + 1] (include/exl3_abi.h:136-141; -1 when no run holds the row). lo / hi: the
+// run clamped to [0, T) (kernels/exl3r4d/launch.c:14-15). Holds a barrier: every thread of the workgroup calls it.
+struct Owner { int e, lo, hi; };
+__device__ Owner owner_wg(const Exl3c4Launch& a, int i) {
+    __shared__ int cnt_s[4];
+    int cnt = 0;
+    for (int e = 1 + (int)threadIdx.x; e <= a.n_expert; e += 256) cnt += a.off[e] <= i ? 1 : 0;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
+    if ((threadIdx.x & 63) == 0) cnt_s[threadIdx.x >> 6] = cnt;
     __syncthreads();
-    int4* ent = (int4*)(a.plan + 4);
-    for (int base = 0; base < a.n_expert; base += 256) {
-        const int e = base + tid;
-        int lo = 0, hi = 0, n = 0;
-        if (e < a.n_expert) {
-            lo = min(max(a.off[e], 0), a.T);
-            hi = min(max(a.off[e + 1], lo), a.T);
-            n = (hi - lo + EXL3C4_CHUNK_ROWS - 1) / EXL3C4_CHUNK_ROWS;
-        }
-        scan[tid] = n;
-        __syncthreads();
-        for (int d = 1; d < 256; d <<= 1) {   // inclusive scan
-            const int t = tid >= d ? scan[tid - d] : 0;
-            __syncthreads();
-            scan[tid] += t;
-            __syncthreads();
-        }
-        const int carry = carry_s;
-        const int first = carry + scan[tid] - n;
-        for (int q = 0; q < n; ++q) {
-            const int at = first + q;
-            if (at < a.max_chunks) {
-                const int r0 = lo + q * EXL3C4_CHUNK_ROWS;
-                ent[at] = make_int4(e, r0, min(EXL3C4_CHUNK_ROWS, hi - r0), 0);
-            }
-        }
-        __syncthreads();
-        if (tid == 255) carry_s = carry + scan[255];
-        __syncthreads();
-    }
-    if (tid == 0) a.plan[0] = min(carry_s, a.max_chunks);
+    const int e = min(cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3], a.n_expert - 1);
+    const int o0 = a.off[e], o1 = a.off[e + 1];
+    Owner w;
+    w.e = (o0 <= i && i < o1) ? e : -1;
+    w.lo = max(o0, 0);
+    w.hi = min(o1, a.T);
+    return w;
 }
 
-// Zero one 128-column block of output row i when no GEMM epilogue writes it: a dead row (outside the runs, or
-// sorted_tok < 0: include/exl3_abi.h:125-134) or a narrower class's tail.
-__device__ void zero_block(const Exl3c4Launch& a, int64_t i, int b, int lane) {
-    int e;
-    const int dead = dead_row(a, (int)i, lane, &e);
-    if (!dead && b * 128 < a.z_width[class_of(a, e)]) return;
-    uint16_t* out = (uint16_t*)a.z + i * a.z_pitch + b * 128;
-    out[lane] = 0;
-    out[lane + 64] = 0;
+// A chunk is at most 16 rows of one run, cut from the run's first row: the workgroup keyed on the chunk's first row
+// does the chunk. Rows of the chunk: 0 when row i does not start one.
+__device__ __forceinline__ int chunk_rows(const Owner& w, int i) {
+    return (w.e >= 0 && ((i - w.lo) & (EXL3C4_CHUNK_ROWS - 1)) == 0) ? min(EXL3C4_CHUNK_ROWS, w.hi - i) : 0;
 }
 
-// One (sorted row i, half m, 128-block b) of the input rotation xr = f16(had(f16(x * s))). Rows outside every run
-// are not written (include/exl3_abi.h:273-278); a run's row whose sorted_tok is negative is written zero.
-__device__ void prep_block(const Exl3c4Launch& a, int64_t i, int m, int b, int lane) {
+// f16(had128(f16(v * s))) over one 128-block, lane l holding k = l (0) and l + 64 (1) (kernels/exl3ref/ref.c:27-32).
+__device__ __forceinline__ void rotate_block(float f0, float f1, uint16_t s0, uint16_t s1, int lane, uint16_t& o0,
+                                             uint16_t& o1) {
+    float v0 = h2f(f2h(f0 * h2f(s0))), v1 = h2f(f2h(f1 * h2f(s1)));
+    had128_wave(v0, v1, lane);
+    o0 = f2h(v0);
+    o1 = f2h(v1);
+}
+
+__device__ __forceinline__ uint16_t ldg16(const void* p, int64_t idx) {
+    return ((const __attribute__((address_space(1))) uint16_t*)p)[idx];
+}
+
+// A staged row's 128-block in LDS, permuted so that each A operand of a step is one ds_read_b128.
+__device__ __forceinline__ void lds_put(uint16_t* A, int q, int kp, int col0, int lane, uint16_t v0, uint16_t v1) {
+    const int o = perm_slot(lane);
+    A[q * kp + col0 + o] = v0;
+    A[q * kp + col0 + o + 64] = v1;
+}
+
+// prep_gu: one wave per (sorted row i, half m, 128-block b): xr = f16(had128(f16(x * s))) with s = suh (m = 0) or suh1
+// (m = 1) of the row's expert. Rows outside every run are not written (include/exl3_abi.h:273-278); a run's row whose
+// sorted_tok is negative is written zero.
+__global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nb = a.x_cols_max / 128;
+    if (wid >= (int64_t)a.T * 2 * nb) return;
+    const int b = (int)(wid % nb);
+    const int64_t im = wid / nb;
+    const int64_t i = im / 2;
+    const int m = (int)(im % 2);
     const int e = owner_wave(a.off, a.n_expert, (int)i, lane);
     if (e < 0) return;
     const int c = class_of(a, e);
@@ -351,48 +349,24 @@ __device__ void prep_block(const Exl3c4Launch& a, int64_t i, int m, int b, int l
     const Exl3c4Class& K = a.cls[c];
     const int C = K.cols;
     if (b * 128 >= C) return;
-    const uint16_t* s = (const uint16_t*)(m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx));
     uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C + b * 128;
-    const int k0 = a.prep_perm ? perm_slot(lane) : lane, k1 = k0 + 64;
     const int tok = a.sorted[i];
     if (tok < 0) {
-        out[k0] = 0;
-        out[k1] = 0;
+        out[lane] = 0;
+        out[lane + 64] = 0;
         return;
     }
-    int64_t src = a.prep_mode == EXL3C4_PREP_DN ? i : tok / a.top_k;
+    int64_t src = tok / a.top_k;
     src = src < a.x_rows ? src : a.x_rows - 1;
-    const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch + b * 128;
-    const uint16_t x0 = x[lane], x1 = x[64 + lane];
+    const void* x = (const uint16_t*)a.x + src * a.x_pitch + b * 128;
+    const void* s = m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    const uint16_t x0 = ldg16(x, lane), x1 = ldg16(x, 64 + lane);
     const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
     const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
-    float v0 = h2f(f2h(f0 * h2f(s[b * 128 + lane])));
-    float v1 = h2f(f2h(f1 * h2f(s[b * 128 + 64 + lane])));
-    had128_wave(v0, v1, lane);
-    out[k0] = f2h(v0);
-    out[k1] = f2h(v1);
-}
-
-// The front of a launch: workgroup 0 plans the chunks and zeroes the counters; then one wave per 128-block of the
-// output rows no epilogue will write (zeroed), then one wave per (row, half, 128-block) of the input rotation.
-__global__ __launch_bounds__(256) void k_front(const Exl3c4Launch a) {
-    if (blockIdx.x == 0) {
-        if (a.do_plan) plan_block(a);
-        return;
-    }
-    const int lane = threadIdx.x & 63;
-    int64_t wid = (int64_t)(blockIdx.x - 1) * 4 + (threadIdx.x >> 6);
-    const int zb = a.z_cols / 128;
-    if (wid < a.zero_waves) {
-        zero_block(a, wid / zb, (int)(wid % zb), lane);
-        return;
-    }
-    wid -= a.zero_waves;
-    const int nb = a.x_cols_max / 128;
-    if (wid >= (int64_t)a.T * a.prep_halves * nb) return;
-    const int b = (int)(wid % nb);
-    const int64_t im = wid / nb;
-    prep_block(a, im / a.prep_halves, (int)(im % a.prep_halves), b, lane);
+    uint16_t o0, o1;
+    rotate_block(f0, f1, ldg16(s, b * 128 + lane), ldg16(s, b * 128 + 64 + lane), lane, o0, o1);
+    out[lane] = o0;
+    out[lane + 64] = o1;
 }
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
@@ -430,9 +404,6 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
         }
     }
 }
-__device__ __forceinline__ uint16_t ldg16(const void* p, int idx) {
-    return ((const __attribute__((address_space(1))) uint16_t*)p)[idx];
-}
 
 // gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
 // sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
@@ -468,86 +439,103 @@ __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c
     v1 = f2h(r1);
 }
 
-// The epilogue of one 128-column block b of gate_up's output row i (class c, entry jx).
-__device__ void epilogue_row(const Exl3c4Launch& a, int64_t i, int b, int c, int64_t jx, int lane) {
-    uint16_t v0, v1;
-    gate_up_block(a, a.cls[c], i, b, jx, a.h_rot, lane, v0, v1);
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
-    const int o0 = a.out_perm ? perm_slot(lane) : lane;
-    out[o0] = v0;
-    out[o0 + 64] = v1;
+typedef const uint32_t __attribute__((address_space(1)))* gu32p;
+
+// One step of the decode GEMV: the wave's segment decoded into B operands and the four MFMAs against the staged rows
+// (arow: this lane's row and k group in LDS).
+template <int BITS, int CB>
+__device__ __forceinline__ void mma_step(const uint32_t (&d)[BITS], const uint16_t* arow, const Mul1Consts& k,
+                                         float4_t& acc0, float4_t& acc1) {
+    uint32_t B[16];
+    decode_segment<BITS, CB>(d, B, k);
+    const half8_t Aa = *(const half8_t*)(arow);
+    const half8_t Ab = *(const half8_t*)(arow + 8);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
 }
 
-// gemv: one wave per unit (chunk, 32-column strip, k split). The unit's partial sums of its strip for the chunk's
-// rows go to part[split][row][col]; the epilogue adds the splits in a fixed order, so the bits do not depend on
-// scheduling. PERM: the activation rows are stored permuted (perm_slot), so each A operand is one 16-byte load.
-typedef const uint32_t __attribute__((address_space(1)))* gu32p;
-typedef const uint16_t __attribute__((address_space(1)))* gu16p;
+// The wave's strip over `ksn` steps (even, or 0) of its stream `rec`, whose first two steps' words are already in dA /
+// dB, against the rows staged in LDS; two steps of words in flight while one is decoded.
+template <int BITS, int CB>
+__device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, uint32_t (&dA)[BITS], uint32_t (&dB)[BITS],
+                                           const uint16_t* arow, float4_t& acc0, float4_t& acc1) {
+    const Mul1Consts k = mul1_consts();
+    for (int s = 0; s < ksn; s += 2) {
+        mma_step<BITS, CB>(dA, arow + s * EXL3C4_KSTEP, k, acc0, acc1);
+        if (s + 2 < ksn) load_words<BITS>(rec + (s + 2) * 64 * BITS, dA);
+        mma_step<BITS, CB>(dB, arow + (s + 1) * EXL3C4_KSTEP, k, acc0, acc1);
+        if (s + 3 < ksn) load_words<BITS>(rec + (s + 3) * 64 * BITS, dB);
+    }
+}
 
-template <int BITS, int CB, bool PERM>
-__global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63;
-    // grid: y = chunk, x * 4 + wave = strip * S + split (S a power of two)
-    const int chunk = blockIdx.y;
-    const int nch = min(a.plan[0], a.max_chunks);
-    if (chunk >= nch) return;
-    const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+// gate_up's GEMM: one workgroup per (sorted row i, group of four 32-column strips, k split). The workgroup keyed on
+// a chunk's first row takes the chunk (at most 16 rows); the others leave. Its four waves take the group's four
+// strips over the split's 128-blocks of k; the split's input rows -- rotated here, f16(had128(f16(x * suh or suh1)))
+// of the token's row, or read as given (a_rot) -- are staged once in LDS for all four. The strip's sums go to
+// part[split][row][col]; their consumer adds the splits in a fixed order, so the bits do not depend on scheduling.
+// Workgroup x = 0 of each row records the row's owner and chunk rows in row_info for the kernels that follow.
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_gu(const Exl3c4Launch a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int i = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int S = a.ksplit;
-    const int strip = u >> a.ksplit_log2, split = u & (S - 1);
-    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
-    const int e = ent.x, row0 = ent.y, nrows = ent.z;
-    const int c = class_of(a, e);
-    const int64_t jx = entry_of(a, e);
+    const int grp = (int)(blockIdx.x >> a.ksplit_log2), split = (int)(blockIdx.x & (S - 1));
+    const Owner w = owner_wg(a, i);
+    const int nrows = chunk_rows(w, i);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        a.row_info[2 * i] = w.e;
+        a.row_info[2 * i + 1] = nrows;
+    }
+    if (nrows == 0) return;
+    const int c = class_of(a, w.e);
+    const int64_t jx = entry_of(a, w.e);
     const Exl3c4Class& K = a.cls[c];
     const int N = K.rows, KC = K.cols;
-    if (strip * EXL3C4_STRIP >= N) return;
-    const int ksteps = KC / EXL3C4_KSTEP;
-    const int per = (ksteps + S - 1) / S;
-    const int ks0 = split * per, ks1 = min(ksteps, ks0 + per);
-
-    const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
-    // A: the row of this lane's token; a lane past the chunk's rows reads a clamped row whose products land only in
-    // output rows that are never stored
-    const int r = lane & 15, g = lane >> 4;
-    const int i = min(row0 + r, a.T - 1);
-    const bool up = a.gate_up && strip * EXL3C4_STRIP >= N / 2;
-    const gu16p arow = (gu16p)a.a + (int64_t)i * a.a_pitch + (up ? KC : 0) + 16 * g;
-
-    const Mul1Consts k = mul1_consts();
-    float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    auto load_step = [&](int ks, uint32_t (&d)[BITS], u32x4_t& c0, u32x4_t& c1) {
-        load_words<BITS>(rec + ks * 64 * BITS, d);
-        c0 = *(const __attribute__((address_space(1))) u32x4_t*)(arow + ks * EXL3C4_KSTEP);
-        c1 = *(const __attribute__((address_space(1))) u32x4_t*)(arow + ks * EXL3C4_KSTEP + 8);
-    };
-    auto mma_step = [&](const uint32_t (&d)[BITS], const u32x4_t& c0, const u32x4_t& c1) {
-        uint32_t B[16];
-        decode_segment<BITS, CB>(d, B, k);
-        half8_t Aa, Ab;
-        if constexpr (PERM) {
-            Aa = __builtin_bit_cast(half8_t, c0);
-            Ab = __builtin_bit_cast(half8_t, c1);
-        } else {
-            Aa = as_half8(c0.x, c1.x, c0.y, c1.y);
-            Ab = as_half8(c0.z, c1.z, c0.w, c1.w);
-        }
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
-    };
-    // two steps in flight: the next step's loads are issued before this step's decode
+    if (grp * 128 >= N) return;
+    const int strip = grp * 4 + wave;
+    const bool up = grp * 128 >= N / 2;
+    const int nb = KC / 128, per = (nb + S - 1) / S;
+    const int b0 = min(nb, split * per), b1 = min(nb, b0 + per);
+    const int ksn = 2 * (b1 - b0);
+    const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_stride, jx) +
+                      ((int64_t)strip * (KC / EXL3C4_KSTEP) + 2 * b0) * 64 * BITS + lane * BITS;
     uint32_t dA[BITS], dB[BITS];
-    u32x4_t a0, a1, b0, b1;
-    int ks = ks0;
-    if (ks < ks1) load_step(ks, dA, a0, a1);
-    for (; ks + 1 < ks1; ks += 2) {
-        load_step(ks + 1, dB, b0, b1);
-        mma_step(dA, a0, a1);
-        if (ks + 2 < ks1) load_step(ks + 2, dA, a0, a1);
-        mma_step(dB, b0, b1);
+    if (ksn > 0) {                                                // its first two steps' words fly during the staging
+        load_words<BITS>(rec, dA);
+        load_words<BITS>(rec + 64 * BITS, dB);
     }
-    if (ks < ks1) mma_step(dA, a0, a1);
+
+    const int kp = a.lds_pitch;
+    uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
+    const void* sv = up ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    for (int q = 0; q < nrows; ++q) {
+        const int64_t r = i + q;
+        const int tok = a.a_rot ? 0 : a.sorted[r];
+        int64_t src = a.a_rot ? r : tok / a.top_k;
+        src = src < a.x_rows ? src : a.x_rows - 1;
+        for (int hb = b0 + wave; hb < b1; hb += 4) {
+            uint16_t v0 = 0, v1 = 0;
+            if (a.a_rot) {
+                const void* xs = (const uint16_t*)a.x + src * a.x_pitch + (up ? KC : 0) + hb * 128;
+                v0 = ldg16(xs, lane);
+                v1 = ldg16(xs, lane + 64);
+            } else if (tok >= 0) {
+                const void* xs = (const uint16_t*)a.x + src * a.x_pitch + hb * 128;
+                const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
+                const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
+                const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
+                rotate_block(f0, f1, ldg16(sv, hb * 128 + lane), ldg16(sv, hb * 128 + 64 + lane), lane, v0, v1);
+            }
+            lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
+        }
+    }
+    __syncthreads();
+
+    float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
+    gemv_strip<BITS, CB>(rec, ksn, dA, dB, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // D lane l: column l % 16 (c' = 2 s + t -> weight row 32 nb + 16 t + s, + 8 for acc1), rows 4 (l / 16) + 0..3
     const int cc = lane & 15, rg = lane >> 4;
@@ -557,52 +545,76 @@ __global__ __launch_bounds__(256) void k_gemv(const Exl3c4Launch a) {
     for (int q = 0; q < 4; ++q) {
         const int tok = rg * 4 + q;
         if (tok < nrows) {
-            pp[(int64_t)(row0 + tok) * a.part_pitch + n] = acc0[q];
-            pp[(int64_t)(row0 + tok) * a.part_pitch + n + 8] = acc1[q];
+            pp[(int64_t)(i + tok) * a.part_pitch + n] = acc0[q];
+            pp[(int64_t)(i + tok) * a.part_pitch + n + 8] = acc1[q];
         }
     }
-
 }
 
-// epilogue: one wave per (chunk, 128-column output block b): the chunk's live rows of that block, from the partial
-// sums of the GEMM that ran before it (the kernel boundary orders and publishes them). Dead rows and a narrower class's
-// tail were zeroed by the front.
-__global__ __launch_bounds__(256) void k_epilogue(const Exl3c4Launch a) {
+// gate_up's epilogue (gate_up alone): one wave per (sorted row i, 128-column block b) of h, from the partial sums.
+// A row no run holds, a negative sorted_tok and a narrower class's tail are written zero.
+__global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= (int64_t)a.T * a.nblk) return;
     const int b = (int)(wid % a.nblk);
-    const int64_t chunk = wid / a.nblk;
-    const int nch = min(a.plan[0], a.max_chunks);
-    if (chunk >= nch) return;
-    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
-    const int e = ent.x, row0 = ent.y, nrows = ent.z;
-    const int c = class_of(a, e);
-    if (b * 128 >= a.cls[c].rows / 2) return;
-    for (int q = 0; q < nrows; ++q) {
-        if (a.sorted[row0 + q] < 0) continue;
-        epilogue_row(a, row0 + q, b, c, entry_of(a, e), lane);
+    const int64_t i = wid / a.nblk;
+    const int e = a.row_info[2 * i];
+    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
+    const int c = e >= 0 ? class_of(a, e) : 0;
+    if (e < 0 || a.sorted[i] < 0 || b * 128 >= a.cls[c].rows / 2) {
+        out[lane] = 0;
+        out[lane + 64] = 0;
+        return;
     }
+    uint16_t v0, v1;
+    gate_up_block(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
+    out[lane] = v0;
+    out[lane + 64] = v1;
 }
 
-// down, one workgroup per (chunk, 128-column output block b): its four waves take the block's four 32-column strips
-// over all of k, so the block's output is whole inside the workgroup and its epilogue (had128, x svh, bf16) runs
-// there. The chunk's input rows are staged in LDS first (permuted, so each A operand is one ds_read_b128): gate_up's
-// h_rot = 1 output computed here from gate_up's partial sums (gate_up_down), or the rows of `a` (down alone). The
-// raw accumulations also go to `dacc` (a checker's view of the sums before any narrowing).
+// down, one workgroup per (sorted row i, 128-column output block b); the workgroup keyed on a chunk's first row takes
+// the chunk. Its four waves take the block's four 32-column strips over all of k, so the block's output is whole
+// inside the workgroup and its epilogue (had128, x svh, bf16) runs there. The chunk's input rows are staged in LDS
+// first: gate_up's h_rot = 1 output computed from gate_up's partial sums (gate_up_down), or the rows of x, rotated
+// (h_rot = 0) or as given (down alone). The raw accumulations also go to `dacc` (a checker's view of the sums before
+// any narrowing). Every (row, block) of y is written once: a row no run holds, a negative sorted_tok and a narrower
+// class's tail as zero.
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_dn(const Exl3c4Launch a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    const int b = blockIdx.x, chunk = blockIdx.y;
+    const int b = blockIdx.x, i = blockIdx.y;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nch = min(a.plan[0], a.max_chunks);
-    if (chunk >= nch) return;
-    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
-    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    int e, nrows;
+    if (a.row_info) {
+        e = a.row_info[2 * i];
+        nrows = a.row_info[2 * i + 1];
+    } else {
+        const Owner w = owner_wg(a, i);
+        e = w.e;
+        nrows = chunk_rows(w, i);
+    }
+    if (e < 0) {
+        if (wave == 0) {
+            uint16_t* out = (uint16_t*)a.y + (int64_t)i * a.y_pitch + b * 128;
+            out[lane] = 0;
+            out[lane + 64] = 0;
+        }
+        return;
+    }
+    if (nrows == 0) return;
     const int c = class_of(a, e);
     const int64_t jx = entry_of(a, e);
     const Exl3c4Class& D = a.cls[c];
     const int N = D.rows, KC = D.cols;
-    if (b * 128 >= N) return;
+    if (b * 128 >= N) {                                           // a narrower class's tail
+        for (int q = wave; q < nrows; q += 4) {
+            uint16_t* out = (uint16_t*)a.y + (int64_t)(i + q) * a.y_pitch + b * 128;
+            out[lane] = 0;
+            out[lane + 64] = 0;
+        }
+        return;
+    }
     const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
     uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
     float* acc_l = (float*)(lds + 16 * kp * 2);                   // [16][128]
@@ -614,51 +626,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     uint32_t dA[BITS], dB[BITS];
     load_words<BITS>(rec, dA);
     load_words<BITS>(rec + 64 * BITS, dB);                       // k is at least 128: two steps
+    const void* svh = tab_entry(D.svh, D.svh_stride, jx);
+    const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
+    const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_stride, jx) : nullptr;
 
     // stage the chunk's rows
     const int nhb = KC / 128;
     for (int q = 0; q < nrows; ++q) {
-        const int64_t i = row0 + q;
+        const int64_t r = i + q;
         for (int hb = wave; hb < nhb; hb += 4) {
-            uint16_t v0, v1;
+            uint16_t v0 = 0, v1 = 0;
             if (a.h_from_gu) {
-                if (a.sorted[i] < 0) continue;                     // its outputs are never stored
-                gate_up_block(a, a.gcls[c], i, hb, jx, 1, lane, v0, v1);
-                const int o = perm_slot(lane);
-                A[q * kp + hb * 128 + o] = v0;
-                A[q * kp + hb * 128 + o + 64] = v1;
+                if (a.sorted[r] >= 0) gate_up_block(a, a.gcls[c], r, hb, jx, 1, lane, v0, v1);
             } else {
-                const uint16_t* src = (const uint16_t*)a.a + i * a.a_pitch + hb * 128;
-                const int o = a.a_perm ? lane : perm_slot(lane);    // scratch rows are already permuted
-                A[q * kp + hb * 128 + o] = src[lane];
-                A[q * kp + hb * 128 + o + 64] = src[lane + 64];
+                const void* xs = (const uint16_t*)a.x + r * a.x_pitch + hb * 128;
+                const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
+                if (a.h_rot) {
+                    v0 = x0;
+                    v1 = x1;
+                } else {
+                    rotate_block(h2f(x0), h2f(x1), ldg16(suh, hb * 128 + lane), ldg16(suh, hb * 128 + 64 + lane), lane,
+                                 v0, v1);
+                }
             }
+            lds_put(A, q, kp, hb * 128, lane, v0, v1);
         }
     }
     __syncthreads();
 
-    const int r = lane & 15, g = lane >> 4;
-    const uint16_t* arow = A + r * kp + 16 * g;
-    const Mul1Consts k = mul1_consts();
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    auto mma_step = [&](const uint32_t (&d)[BITS], int ks) {
-        uint32_t B[16];
-        decode_segment<BITS, CB>(d, B, k);
-        const half8_t Aa = *(const half8_t*)(arow + ks * EXL3C4_KSTEP);
-        const half8_t Ab = *(const half8_t*)(arow + ks * EXL3C4_KSTEP + 8);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
-    };
-    int ks = 0;
-    for (; ks + 1 < ksteps; ks += 2) {
-        mma_step(dA, ks);
-        if (ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dA);
-        mma_step(dB, ks + 1);
-        if (ks + 3 < ksteps) load_words<BITS>(rec + (ks + 3) * 64 * BITS, dB);
-    }
-    if (ks < ksteps) mma_step(dA, ks);
+    gemv_strip<BITS, CB>(rec, ksteps, dA, dB, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // the block's accumulations to LDS (column of D lane l: 16 (l & 1) + (l / 2) within the strip, + 8 for acc1)
     const int cc = lane & 15, rg = lane >> 4;
@@ -673,18 +670,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     }
     __syncthreads();
 
-    const uint16_t* svh = (const uint16_t*)tab_entry(D.svh, D.svh_stride, jx);
     for (int q = wave; q < nrows; q += 4) {
-        const int64_t i = row0 + q;
+        const int64_t r = i + q;
         float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
-        float* dacc = a.dacc + i * a.dacc_pitch + b * 128;
+        float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
         dacc[lane] = y0;
         dacc[lane + 64] = y1;
-        if (a.sorted[i] < 0) continue;                             // zeroed by the front
+        uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
+        if (a.sorted[r] < 0) {
+            out[lane] = 0;
+            out[lane + 64] = 0;
+            continue;
+        }
         had128_wave(y0, y1, lane);
-        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
-        out[lane] = f2bf(y0 * h2f(svh[b * 128 + lane]));
-        out[lane + 64] = f2bf(y1 * h2f(svh[b * 128 + 64 + lane]));
+        out[lane] = f2bf(y0 * h2f(sv0));
+        out[lane + 64] = f2bf(y1 * h2f(sv1));
     }
 }
 
@@ -716,55 +716,36 @@ __global__ __launch_bounds__(256) void k_dequant(const uint32_t* rec, int rows, 
 
 // ------------------------------------------------------------------------------------------------ dispatch
 
-typedef void (*GemvFn)(const Exl3c4Launch);
+typedef void (*GemmFn)(const Exl3c4Launch);
 typedef void (*DequantFn)(const uint32_t*, int, int, uint16_t*, int64_t);
 
-template <int BITS, bool PERM> GemvFn gemv_fn2(int cb) {
+template <template <int, int> class F, int BITS> GemmFn by_cb(int cb) {
     switch (cb) {
-    case EXL3C4_CB_MUL1: return k_gemv<BITS, EXL3C4_CB_MUL1, PERM>;
-    case EXL3C4_CB_MCG:  return k_gemv<BITS, EXL3C4_CB_MCG, PERM>;
-    default:             return k_gemv<BITS, EXL3C4_CB_3INST, PERM>;
+    case EXL3C4_CB_MUL1: return F<BITS, EXL3C4_CB_MUL1>::fn;
+    case EXL3C4_CB_MCG:  return F<BITS, EXL3C4_CB_MCG>::fn;
+    default:             return F<BITS, EXL3C4_CB_3INST>::fn;
     }
 }
-template <int BITS> GemvFn gemv_fn(int cb, bool perm) { return perm ? gemv_fn2<BITS, true>(cb) : gemv_fn2<BITS, false>(cb); }
+template <template <int, int> class F> GemmFn by_bits(int bits, int cb) {
+    switch (bits) {
+    case 2: return by_cb<F, 2>(cb);
+    case 3: return by_cb<F, 3>(cb);
+    case 4: return by_cb<F, 4>(cb);
+    case 5: return by_cb<F, 5>(cb);
+    case 6: return by_cb<F, 6>(cb);
+    case 7: return by_cb<F, 7>(cb);
+    case 8: return by_cb<F, 8>(cb);
+    default: return nullptr;
+    }
+}
+template <int BITS, int CB> struct GuK { static constexpr GemmFn fn = k_gu<BITS, CB>; };
+template <int BITS, int CB> struct DnK { static constexpr GemmFn fn = k_dn<BITS, CB>; };
+
 template <int BITS> DequantFn dequant_fn(int cb) {
     switch (cb) {
     case EXL3C4_CB_MUL1: return k_dequant<BITS, EXL3C4_CB_MUL1>;
     case EXL3C4_CB_MCG:  return k_dequant<BITS, EXL3C4_CB_MCG>;
     default:             return k_dequant<BITS, EXL3C4_CB_3INST>;
-    }
-}
-
-template <int BITS> GemvFn dn_fn(int cb) {
-    switch (cb) {
-    case EXL3C4_CB_MUL1: return k_dn<BITS, EXL3C4_CB_MUL1>;
-    case EXL3C4_CB_MCG:  return k_dn<BITS, EXL3C4_CB_MCG>;
-    default:             return k_dn<BITS, EXL3C4_CB_3INST>;
-    }
-}
-GemvFn pick_dn(int bits, int cb) {
-    switch (bits) {
-    case 2: return dn_fn<2>(cb);
-    case 3: return dn_fn<3>(cb);
-    case 4: return dn_fn<4>(cb);
-    case 5: return dn_fn<5>(cb);
-    case 6: return dn_fn<6>(cb);
-    case 7: return dn_fn<7>(cb);
-    case 8: return dn_fn<8>(cb);
-    default: return nullptr;
-    }
-}
-
-GemvFn pick_gemv(int bits, int cb, bool perm) {
-    switch (bits) {
-    case 2: return gemv_fn<2>(cb, perm);
-    case 3: return gemv_fn<3>(cb, perm);
-    case 4: return gemv_fn<4>(cb, perm);
-    case 5: return gemv_fn<5>(cb, perm);
-    case 6: return gemv_fn<6>(cb, perm);
-    case 7: return gemv_fn<7>(cb, perm);
-    case 8: return gemv_fn<8>(cb, perm);
-    default: return nullptr;
     }
 }
 DequantFn pick_dequant(int bits, int cb) {
@@ -806,31 +787,32 @@ int go2(F f, dim3 grid, hipStream_t s, void* ev0, void* ev1, uint32_t lds, Args.
 
 }  // namespace
 
-extern "C" int exl3c4_dev_front(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->zero_waves + (int64_t)a->T * a->prep_halves * (a->x_cols_max / 128);
-    return go(k_front, 1 + blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
-}
-
-extern "C" int exl3c4_dev_epilogue(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->max_chunks * a->nblk;
+extern "C" int exl3c4_dev_prep(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = (int64_t)a->T * 2 * (a->x_cols_max / 128);
     if (waves <= 0) return 0;
-    return go(k_epilogue, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+    return go(k_prep, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
-extern "C" int exl3c4_dev_gemv(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemvFn f = pick_gemv(a->bits, a->codebook, a->a_perm != 0);
+extern "C" int exl3c4_dev_gu(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemmFn f = by_bits<GuK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
-    const int64_t waves = (int64_t)a->max_strips * a->ksplit;
-    if (waves <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3(blocks_for_waves(waves), a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
+    if (a->T <= 0 || a->n_grp <= 0) return 0;
+    const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2);
+    return go2(f, dim3((unsigned)(a->n_grp * a->ksplit), (unsigned)a->T), (hipStream_t)stream, ev0, ev1, lds, *a);
+}
+
+extern "C" int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = (int64_t)a->T * a->nblk;
+    if (waves <= 0) return 0;
+    return go(k_gepi, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemvFn f = pick_dn(a->bits, a->codebook);
+    const GemmFn f = by_bits<DnK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
-    if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
+    if (a->nblk <= 0 || a->T <= 0) return 0;
     const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2 + 16 * 128 * 4);
-    return go2(f, dim3(a->nblk, a->max_chunks), (hipStream_t)stream, ev0, ev1, lds, *a);
+    return go2(f, dim3((unsigned)a->nblk, (unsigned)a->T), (hipStream_t)stream, ev0, ev1, lds, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

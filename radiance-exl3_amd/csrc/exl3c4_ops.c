@@ -58,40 +58,41 @@ static int log2i(int v) {
 }
 
 typedef struct Carve {
-    int64_t plan, ctr, xr, part, dacc, total;
-    int64_t chunks, T, xr_pitch, part_pitch, dacc_pitch, dn_kmax;
-    int     split_gu, nblk_gu;
+    int64_t row_info, part, dacc, total;
+    int64_t T, part_pitch, dacc_pitch;
+    int     split_gu, gu_lds_pitch, dn_lds_pitch;
 } Carve;
 
-/* The scratch of one launch with T sorted rows: [plan | xr | gate_up partial sums | down accumulations], each region
- * 256-B aligned. */
+/* The scratch of one launch with T sorted rows, each region 256-B aligned: [row_info | gate_up partial sums | down
+ * accumulations]. row_info: the row's owner and chunk rows, written by gate_up's GEMM for the kernels after it. */
 static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     const int op = o->op;
-    const int64_t xc = max_cols(o), rc = max_rows(o);
+    const int64_t rc = max_rows(o);
     memset(k, 0, sizeof *k);
     k->T = T;
-    k->chunks = chunk_bound(T, o->n_expert);
     int64_t off = 0;
-    k->plan = off;
-    off += ALIGN_UP(16 + 16 * k->chunks, 256);
-    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) k->nblk_gu = (int)(rc / 2 / 128);
-    k->ctr = off;
-    k->xr = off;
-    if (op == EXL3C4_GATE_UP && !o->a_rot) k->xr_pitch = 2 * xc;
-    else if (op == EXL3C4_GU_DN) k->xr_pitch = 2 * xc;
-    else if (op == EXL3C4_DOWN && !o->h_rot) k->xr_pitch = xc;
-    off += ALIGN_UP(T * k->xr_pitch * 2, 256);
+    const int gu = op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN;
+    const int dn = op == EXL3C4_DOWN || op == EXL3C4_GU_DN;
+    k->row_info = off;
+    if (gu) off += ALIGN_UP(T * 8, 256);
     k->part = off;
-    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
-        int64_t kmin = INT64_MAX;
-        for (int c = 0; c < o->n_class; ++c)
-            if (o->cls[c].cols / EXL3C4_KSTEP < kmin) kmin = o->cls[c].cols / EXL3C4_KSTEP;
-        k->split_gu = ksplit_for(k->chunks, rc / EXL3C4_STRIP, kmin);
+    if (gu) {
+        /* split-K: from T and the geometry; at most 12 128-blocks of k a split, so the staged rows fit LDS */
+        int64_t nb_min = INT64_MAX, nb_max = 0;
+        for (int c = 0; c < o->n_class; ++c) {
+            const int64_t nb = o->cls[c].cols / 128;
+            if (nb < nb_min) nb_min = nb;
+            if (nb > nb_max) nb_max = nb;
+        }
+        int s = ksplit_for(chunk_bound(T, o->n_expert), rc / EXL3C4_STRIP, 2 * nb_min);
+        while ((nb_max + s - 1) / s > 12) s *= 2;
+        k->split_gu = s;
+        k->gu_lds_pitch = (int)(((nb_max + s - 1) / s) * 128 + 8);
         k->part_pitch = rc;
-        off += ALIGN_UP(k->split_gu * T * rc * 4, 256);
+        off += ALIGN_UP(s * T * rc * 4, 256);
     }
     k->dacc = off;
-    if (op == EXL3C4_DOWN || op == EXL3C4_GU_DN) {
+    if (dn) {
         /* down's geometry: its own classes, or gate_up_down's [cols, rows / 2] */
         int64_t nmax = 0, kmax = 0;
         for (int c = 0; c < o->n_class; ++c) {
@@ -101,7 +102,7 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
             if (kk > kmax) kmax = kk;
         }
         k->dacc_pitch = nmax;
-        k->dn_kmax = kmax;
+        k->dn_lds_pitch = (int)(kmax + 8);     /* padded: the 16 staged rows start in different LDS banks */
         off += ALIGN_UP(T * nmax * 4, 256);
     }
     k->total = off;
@@ -192,7 +193,6 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     memset(a, 0, sizeof *a);
     a->sorted = o->sorted_tok;
     a->off = o->expert_offset;
-    a->plan = (int32_t*)(s + k->plan);
     a->part = (float*)(s + k->part);
     a->part_pitch = k->part_pitch;
     a->part_split = k->T * k->part_pitch;
@@ -200,21 +200,27 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->n_expert = (int32_t)o->n_expert;
     a->top_k = (int32_t)o->top_k;
     a->n_class = o->n_class;
-    a->max_chunks = (int32_t)k->chunks;
     a->bits = o->bits;
     a->codebook = o->codebook;
+    a->x = o->x;
+    a->x_pitch = o->x_pitch;
     a->x_dtype = o->x_dtype;
     a->x_rows = (int32_t)o->x_rows;
     a->x_cols_max = (int32_t)max_cols(o);
+    a->y = o->y;
+    a->y_pitch = o->y_pitch;
+    a->y_cols = (int32_t)o->y_cols;
 }
 
 /* The events of a timed launch go to exactly one kernel of the sequence. */
 typedef struct Timed { int kernel; void *ev0, *ev1; } Timed;
 #define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
 
-/* Every op is at most three launches on the stream: the front (plan, zero rows, input rotation); gate_up's GEMM
- * (and, for gate_up alone, its epilogue); down's GEMM, whose workgroups finish their output blocks themselves and, in
- * gate_up_down, build h from gate_up's partial sums. */
+/* The launches of each op on the stream -- no planning pass: every workgroup finds its rows' expert itself.
+ *   prep_gu       the input rotation
+ *   gate_up       its GEMM (input rotation staged inside), then its epilogue
+ *   down          its GEMM, whose workgroups stage (and rotate) their rows and finish their output blocks
+ *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums */
 static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
@@ -225,55 +231,32 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     if (o->T == 0) return EXL3C4_OK;
     char* s = (char*)scratch;
     const int op = o->op;
-    const int64_t rcw = max_rows(o);
 
-    /* the front */
-    Exl3c4Launch f;
-    base_args(o, &k, s, &f);
-    for (int c = 0; c < o->n_class; ++c) f.cls[c] = o->cls[c];
-    f.x = o->x;
-    f.x_pitch = o->x_pitch;
     if (op == EXL3C4_PREP_GU) {
-        f.y = o->y; f.y_pitch = o->y_pitch;
-        f.prep_mode = EXL3C4_PREP_GU_OP;
-        f.prep_halves = 2;
-        return exl3c4_dev_front(&f, stream, EV(EXL3C4_K_FRONT));
+        Exl3c4Launch f;
+        base_args(o, &k, s, &f);
+        for (int c = 0; c < o->n_class; ++c) f.cls[c] = o->cls[c];
+        return exl3c4_dev_prep(&f, stream, EV(EXL3C4_K_PREP));
     }
-    f.do_plan = 1;
-    f.z = o->y; f.z_pitch = o->y_pitch; f.z_cols = (int32_t)o->y_cols;
-    f.zero_waves = (int32_t)(o->T * (o->y_cols / 128));
-    for (int c = 0; c < o->n_class; ++c)
-        f.z_width[c] = op == EXL3C4_GATE_UP ? o->cls[c].rows / 2 : op == EXL3C4_GU_DN ? o->cls[c].cols : o->cls[c].rows;
-    const int gu_prep = (op == EXL3C4_GATE_UP && !o->a_rot) || op == EXL3C4_GU_DN;
-    const int dn_prep = op == EXL3C4_DOWN && !o->h_rot;
-    if (gu_prep || dn_prep) {
-        f.y = s + k.xr; f.y_pitch = k.xr_pitch;
-        f.prep_mode = gu_prep ? EXL3C4_PREP_GU_SCRATCH : EXL3C4_PREP_DN;
-        f.prep_halves = gu_prep ? 2 : 1;
-        f.prep_perm = 1;
-    }
-    if ((rc = exl3c4_dev_front(&f, stream, EV(EXL3C4_K_FRONT))) != 0) return rc;
 
-    /* gate_up: its GEMM; alone, its epilogue kernel; in gate_up_down, down stages h from its partial sums */
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
         base_args(o, &k, s, &a);
         for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
-        if (gu_prep) { a.a = s + k.xr; a.a_pitch = k.xr_pitch; a.a_perm = 1; }
-        else { a.a = o->x; a.a_pitch = o->x_pitch; }
-        a.gate_up = 1;
+        a.row_info = (int32_t*)(s + k.row_info);
+        a.a_rot = op == EXL3C4_GATE_UP ? o->a_rot : 0;
+        a.h_rot = o->h_rot;
         a.ksplit = k.split_gu;
         a.ksplit_log2 = log2i(k.split_gu);
-        a.max_strips = (int32_t)(rcw / EXL3C4_STRIP);
-        a.nblk = k.nblk_gu;
-        a.y = o->y; a.y_pitch = o->y_pitch; a.y_cols = (int32_t)o->y_cols;
-        a.h_rot = o->h_rot;
-        if ((rc = exl3c4_dev_gemv(&a, stream, EV(EXL3C4_K_GEMV_GU))) != 0) return rc;
-        if (op == EXL3C4_GATE_UP) return exl3c4_dev_epilogue(&a, stream, EV(EXL3C4_K_EPI_GU));
+        a.n_grp = (int32_t)(max_rows(o) / 128);
+        a.lds_pitch = k.gu_lds_pitch;
+        a.nblk = (int32_t)(o->y_cols / 128);
+        if ((rc = exl3c4_dev_gu(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
+        if (op == EXL3C4_GATE_UP) return exl3c4_dev_gepi(&a, stream, EV(EXL3C4_K_EPI_GU));
     }
 
     /* down: its own classes, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
-     * (include/exl3_abi.h:751-800; h crosses rotated), one workgroup per (chunk, 128-column block) */
+     * (include/exl3_abi.h:751-800; h crosses rotated) */
     Exl3c4Launch d;
     base_args(o, &k, s, &d);
     for (int c = 0; c < o->n_class; ++c) {
@@ -290,17 +273,15 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     }
     if (op == EXL3C4_GU_DN) {
         d.h_from_gu = 1;
-        d.ksplit = k.split_gu;                 /* the gate_up partial sums it reads */
-    } else if (dn_prep) {
-        d.a = s + k.xr; d.a_pitch = k.xr_pitch; d.a_perm = 1;
+        d.row_info = (int32_t*)(s + k.row_info);     /* written by gate_up's GEMM */
+        d.ksplit = k.split_gu;                       /* the gate_up partial sums it reads */
     } else {
-        d.a = o->x; d.a_pitch = o->x_pitch;
+        d.h_rot = o->h_rot;
     }
     d.nblk = (int32_t)(o->y_cols / 128);
-    d.lds_pitch = (int32_t)k.dn_kmax + 8;      /* padded: the 16 staged rows start in different LDS banks */
+    d.lds_pitch = k.dn_lds_pitch;
     d.dacc = (float*)(s + k.dacc);
     d.dacc_pitch = k.dacc_pitch;
-    d.y = o->y; d.y_pitch = o->y_pitch; d.y_cols = (int32_t)o->y_cols;
     return exl3c4_dev_dn(&d, stream, EV(EXL3C4_K_DOWN));
 }
 
@@ -311,7 +292,7 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
 
 int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop) {
-    if (kernel < EXL3C4_K_FRONT || kernel > EXL3C4_K_DOWN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
+    if (kernel < EXL3C4_K_PREP || kernel > EXL3C4_K_DOWN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
     const Timed t = { kernel, ev_start, ev_stop };
     return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libexl3c4.so")
 
 DOWN, GATE_UP, PREP_GU, GU_DN = 0, 1, 2, 3
-K_FRONT, K_GEMV_GU, K_EPI_GU, K_DOWN = 0, 1, 2, 3
+K_PREP, K_GATE_UP, K_EPI_GU, K_DOWN = 0, 1, 2, 3
 CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 F16, BF16 = 0, 1
 STATUS = {0: "OK", -1: "RAD_E_SHAPE", -2: "RAD_E_DTYPE", -3: "RAD_E_ALIGN", -4: "RAD_E_STRIDE", -9: "RAD_E_SCHEMA",
