@@ -110,7 +110,7 @@ def cpu_baseline(draw, max_experts, seed):
 
 def read_traffic():
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if there is one."""
-    p = os.path.join(ROOT, "profiles", "traffic_gemv_gu_decode.json")
+    p = os.path.join(ROOT, "profiles", "traffic_k_gu_decode.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -126,6 +126,8 @@ def main():
     ap.add_argument("--draws", type=int, default=8)
     ap.add_argument("--cpu-experts", type=int, default=24, help="live experts in the CPU-baseline sample (0: skip)")
     ap.add_argument("--seed", type=int, default=20261013)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run 20 plain device-to-device copies of BYTES (the HBM-counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on ONE GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
@@ -133,6 +135,14 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_probe > 0:
+        src = torch.empty(args.copy_probe, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe, "copies": 20}), flush=True)
+        return
     import exl3c4
     exl3c4.lib()
     torch.cuda.set_device(0)
@@ -183,8 +193,10 @@ def main():
     layer_bytes = float(np.mean(live)) * EXPERT_BYTES
     layer_gbps = layer_bytes / (ms_step * 1e-3) / 1e9
 
-    # the dominant kernel (gate_up's GEMV), live: events stamped by its own dispatch, eager steps
+    # the dominant kernel (gate_up's GEMM), live: events stamped around its own dispatch, eager steps queued behind a
+    # short spin so that they run back to back as in the timed region (no host gaps between them)
     evs = [(exl3c4.Event(), exl3c4.Event()) for _ in range(args.steps)]
+    torch.cuda._sleep(int(2e6 + 2e5 * args.steps))
     for i in range(args.steps):
         a, b = evs[i]
         rc = exl3c4.launch_timed(ops[i % len(ops)], scratch, exl3c4.K_GATE_UP, a, b, stream)
@@ -221,7 +233,7 @@ def main():
         "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(),
-                     "kernel": "k_gemv<4,mul1> (gate_up)", "avg_us": round(float(np.mean(durs)) * 1e3, 3),
+                     "kernel": "k_gu<4,mul1> (gate_up GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 3),
                      "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
         "cpu_baseline": cpu,
     }
