@@ -103,6 +103,12 @@ typedef struct Exl3c4Op {
  * geometry): docs/STEP0.md:142-146, kernels/exl3r4d/launch.c:263-275. Negative: the refusal the launch would give. */
 int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
 
+/* The same from the geometry alone (no operands): the op, its classes' [rows, cols] as the op's weights are (for
+ * gate_up_down: gate_up's), M tokens (a band's top), top_k and n_expert. What a plugin's scratch hook answers from
+ * the parameters (docs/STEP0.md:142-146). A negative status for a geometry the op refuses. */
+int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* rows, const int32_t* cols, int64_t M,
+                                  int64_t top_k, int64_t n_expert);
+
 /* Checks, then launches, one op on `stream` (kernels/exl3r4d/launch.c:525-612, 687-790, 833-855). Nothing is written
  * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);

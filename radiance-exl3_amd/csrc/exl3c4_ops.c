@@ -187,6 +187,30 @@ int64_t exl3c4_scratch_bytes(const Exl3c4Op* o) {
     return k.total;
 }
 
+int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* rows, const int32_t* cols, int64_t M,
+                                  int64_t top_k, int64_t n_expert) {
+    Exl3c4Op q;
+    Carve k;
+    if (op < EXL3C4_DOWN || op > EXL3C4_GU_DN || !rows || !cols) return EXL3C4_E_INVAL;
+    if (n_class != 1 && n_class != 2 && n_class != 4) return EXL3C4_E_INVAL;
+    if (M < 1 || top_k < 1 || n_expert < 1 || n_expert > 65536) return EXL3C4_E_SHAPE;
+    memset(&q, 0, sizeof q);
+    q.op = op;
+    q.n_class = n_class;
+    q.M = M;
+    q.top_k = top_k;
+    q.n_expert = n_expert;
+    for (int c = 0; c < n_class; ++c) {
+        if (cols[c] <= 0 || cols[c] % 128) return EXL3C4_E_SHAPE;
+        if (op != EXL3C4_PREP_GU && (rows[c] <= 0 || rows[c] % (is_gate_up(op) ? 256 : 128))) return EXL3C4_E_SHAPE;
+        if ((op == EXL3C4_DOWN ? cols[c] : op == EXL3C4_GU_DN ? rows[c] / 2 : 0) > 1536) return EXL3C4_E_UNSUPPORTED;
+        q.cls[c].rows = rows[c];
+        q.cls[c].cols = cols[c];
+    }
+    carve(&q, M * top_k, &k);
+    return k.total;
+}
+
 /* ------------------------------------------------------------------ the launch */
 
 static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* a) {
