@@ -17,6 +17,8 @@ extern "C" {
 /* Columns one wave's strip holds (two 16-column tiles) and k one step consumes (four 16-k tiles). */
 #define EXL3C4_STRIP 32
 #define EXL3C4_KSTEP 64
+/* Rows of one chunk on the prefill path (four MFMA row tiles decode-shared). */
+#define EXL3C4_PF_ROWS 64
 
 typedef struct Exl3c4Launch {
     Exl3c4Class    cls[4];        /* the GEMM's weight classes (gate_up's, or down's); prep: the scale source */
@@ -43,6 +45,9 @@ typedef struct Exl3c4Launch {
     int32_t        nblk;          /* epilogue / down: 128-column output blocks a row */
     int32_t        lds_pitch;     /* halves a staged input row in LDS */
     int32_t        y_cols;
+    int32_t*       plan;          /* prefill: [0] chunk count, then int4 {expert, row0, rows, 0} per chunk */
+    int32_t        max_chunks;
+    int32_t        blk_per_wave;  /* gate_up's epilogue: 128-blocks of a row one wave takes */
 } Exl3c4Launch;
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the
@@ -51,6 +56,13 @@ int exl3c4_dev_prep(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gu(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+/* the prefill path */
+int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
                        int64_t w_pitch, void* stream);
 

@@ -556,21 +556,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (wid >= (int64_t)a.T * a.nblk) return;
-    const int b = (int)(wid % a.nblk);
-    const int64_t i = wid / a.nblk;
+    const int per = max(1, a.blk_per_wave), nw = (a.nblk + per - 1) / per;   // a wave takes `per` blocks of a row
+    if (wid >= (int64_t)a.T * nw) return;
+    const int64_t i = wid / nw;
+    const int b0 = (int)(wid % nw) * per, b1 = min(a.nblk, b0 + per);
     const int e = a.row_info[2 * i];
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
     const int c = e >= 0 ? class_of(a, e) : 0;
-    if (e < 0 || a.sorted[i] < 0 || b * 128 >= a.cls[c].rows / 2) {
-        out[lane] = 0;
-        out[lane + 64] = 0;
-        return;
+    const bool dead = e < 0 || a.sorted[i] < 0;
+    for (int b = b0; b < b1; ++b) {
+        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
+        uint16_t v0 = 0, v1 = 0;
+        if (!dead && b * 128 < a.cls[c].rows / 2) gate_up_block(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
+        out[lane] = v0;
+        out[lane + 64] = v1;
     }
-    uint16_t v0, v1;
-    gate_up_block(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
-    out[lane] = v0;
-    out[lane + 64] = v1;
 }
 
 // down, one workgroup per (sorted row i, 128-column output block b); the workgroup keyed on a chunk's first row takes
@@ -688,6 +687,311 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     }
 }
 
+// ------------------------------------------------------------------------------------------------ the prefill path
+//
+// Many rows an expert: each weight is decoded once per chunk of up to 64 rows of its run and fed to 4 row tiles of
+// MFMAs. The launches: a plan (the chunks, and each row's owner), the input rotation into scratch (xr, as prep_gu
+// writes it, or down's rotated h), the GEMMs, and the epilogues.
+
+// One workgroup: every expert's run clamped to [0, T) cut into chunks of at most 64 rows, in expert order
+// (kernels/exl3r4d/launch.c:14-15 clamps the runs).
+__global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
+    __shared__ int scan[1024];
+    __shared__ int carry_s;
+    const int tid = threadIdx.x;
+    if (tid == 0) carry_s = 0;
+    __syncthreads();
+    int4* ent = (int4*)(a.plan + 4);
+    for (int base = 0; base < a.n_expert; base += 1024) {
+        const int e = base + tid;
+        int lo = 0, hi = 0, n = 0;
+        if (e < a.n_expert) {
+            lo = min(max(a.off[e], 0), a.T);
+            hi = min(max(a.off[e + 1], lo), a.T);
+            n = (hi - lo + EXL3C4_PF_ROWS - 1) / EXL3C4_PF_ROWS;
+        }
+        scan[tid] = n;
+        __syncthreads();
+        for (int d = 1; d < 1024; d <<= 1) {                     // inclusive scan
+            const int t = tid >= d ? scan[tid - d] : 0;
+            __syncthreads();
+            scan[tid] += t;
+            __syncthreads();
+        }
+        const int first = carry_s + scan[tid] - n;
+        for (int q = 0; q < n; ++q) {
+            const int at = first + q;
+            if (at < a.max_chunks) {
+                const int r0 = lo + q * EXL3C4_PF_ROWS;
+                ent[at] = make_int4(e, r0, min(EXL3C4_PF_ROWS, hi - r0), 0);
+            }
+        }
+        __syncthreads();
+        if (tid == 1023) carry_s += scan[1023];
+        __syncthreads();
+    }
+    if (tid == 0) a.plan[0] = min(carry_s, a.max_chunks);
+}
+
+// The rotation into scratch, one wave per (sorted row, half, 128-block): gate_up's xr (halves 0 and 1: suh, suh1 of
+// the row's expert, token rows in) or down's rotated h (half 0: down's suh, sorted rows in). Rows no run holds are
+// not written (nothing reads them); a negative sorted_tok gives zeros.
+__global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
+    if (wid >= (int64_t)a.T * halves) return;
+    const int64_t i = wid / halves;
+    const int m = (int)(wid % halves);
+    const int e = a.row_info[2 * i];
+    if (e < 0) return;
+    const Exl3c4Class& K = a.cls[class_of(a, e)];
+    const int64_t jx = entry_of(a, e);
+    const int C = K.cols;
+    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C;
+    const int tok = a.sorted[i];
+    if (tok < 0) {
+        for (int b = 0; b < C / 128; ++b) {
+            out[b * 128 + lane] = 0;
+            out[b * 128 + lane + 64] = 0;
+        }
+        return;
+    }
+    int64_t src = halves == 2 ? tok / a.top_k : i;
+    src = src < a.x_rows ? src : a.x_rows - 1;
+    const void* x = (const uint16_t*)a.x + src * a.x_pitch;
+    const void* sc = m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    const bool bf = halves == 2 && a.x_dtype == EXL3C4_BF16;
+    // two blocks a step: the next block's four loads are out while this one rotates
+    uint16_t x0 = ldg16(x, lane), x1 = ldg16(x, 64 + lane), s0 = ldg16(sc, lane), s1 = ldg16(sc, 64 + lane);
+    for (int b = 0; b < C / 128; ++b) {
+        uint16_t nx0 = 0, nx1 = 0, ns0 = 0, ns1 = 0;
+        if (b + 1 < C / 128) {
+            const int nb0 = (b + 1) * 128;
+            nx0 = ldg16(x, nb0 + lane); nx1 = ldg16(x, nb0 + 64 + lane);
+            ns0 = ldg16(sc, nb0 + lane); ns1 = ldg16(sc, nb0 + 64 + lane);
+        }
+        uint16_t o0, o1;
+        rotate_block(bf ? bf2f(x0) : h2f(x0), bf ? bf2f(x1) : h2f(x1), s0, s1, lane, o0, o1);
+        out[b * 128 + lane] = o0;
+        out[b * 128 + lane + 64] = o1;
+        x0 = nx0; x1 = nx1; s0 = ns0; s1 = ns1;
+    }
+}
+
+// Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows).
+__global__ __launch_bounds__(256) void k_zero_dead(const Exl3c4Launch a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= a.T || a.row_info[2 * i] >= 0) return;
+    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
+    for (int b = 0; b < a.nblk; ++b) {
+        out[b * 128 + lane] = 0;
+        out[b * 128 + lane + 64] = 0;
+    }
+}
+
+// Each row's owner, by a binary search of the runs (clamped to [0, T)) per thread: row_info[i] = {e or -1, 0}.
+__global__ __launch_bounds__(256) void k_rowinfo(const Exl3c4Launch a) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.T) return;
+    // the last e with clamp(off[e]) <= i, over e in [0, n_expert)
+    int lo = 0, hi = a.n_expert - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (min(max(a.off[mid], 0), a.T) <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    const int o0 = min(max(a.off[lo], 0), a.T), o1 = min(max(a.off[lo + 1], o0), a.T);
+    a.row_info[2 * i] = (o0 <= i && i < o1) ? lo : -1;
+    a.row_info[2 * i + 1] = 0;
+}
+
+// Stage one 128-k block of up to 64 rows of a row-major f16 source into LDS, permuted (perm_slot) so that each A
+// operand is one ds_read_b128: thread t takes two 16-groups; a group's first 8 halves (k 0..7) land in dwords 0,2,4,6 of
+// the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` are not loaded.
+struct StageRegs { u32x4_t v[4]; };
+__device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, int row0, int nrows, int col0,
+                                           StageRegs& r) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int g = (int)threadIdx.x + 256 * h;                // 512 groups: row g / 8, 16-group g % 8
+        const int q = g >> 3, grp = g & 7;
+        if (q < nrows) {
+            const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
+                (src + (int64_t)(row0 + q) * pitch + col0 + grp * 16);
+            r.v[2 * h] = p[0];
+            r.v[2 * h + 1] = p[1];
+        }
+    }
+}
+__device__ __forceinline__ void stage_store(uint16_t* A, int kp, int nrows, const StageRegs& r) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int g = (int)threadIdx.x + 256 * h;
+        const int q = g >> 3, grp = g & 7;
+        if (q < nrows) {
+            const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
+            u32x4_t* d = (u32x4_t*)(A + q * kp + grp * 16);
+            d[0] = u32x4_t{ lo.x, hi.x, lo.y, hi.y };
+            d[1] = u32x4_t{ lo.z, hi.z, lo.w, hi.w };
+        }
+    }
+}
+
+// The prefill GEMM of one chunk (<= 64 rows of one expert) against one 128-column group of the weight (4 waves = 4
+// strips), all of k: the input's 128-k blocks stream through two LDS buffers; each wave decodes its strip's step once
+// and runs it against every row tile. Accumulations: acc[row tile][strip half].
+template <int BITS, int CB>
+__device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
+                                        const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
+                                        uint16_t* lds, float4_t (&acc)[4][2]) {
+    const int lane = threadIdx.x & 63;
+    const int KC = W.cols, nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
+    const int kp = 128 + 8;
+    uint16_t* buf[2] = { lds, lds + 64 * kp };
+    const int ntile = (nrows + 15) >> 4;
+    const gu32p rec = (gu32p)tab_entry(W.codes, W.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    uint32_t dA[BITS], dB[BITS];
+    load_words<BITS>(rec, dA);
+    load_words<BITS>(rec + 64 * BITS, dB);
+    StageRegs r;
+    stage_load(src, pitch, row0, nrows, col_off, r);
+    stage_store(buf[0], kp, nrows, r);
+    __syncthreads();
+    const Mul1Consts k = mul1_consts();
+    const int rr = lane & 15, g = lane >> 4;
+    for (int kb = 0; kb < nb; ++kb) {
+        if (kb + 1 < nb) stage_load(src, pitch, row0, nrows, col_off + (kb + 1) * 128, r);
+        const uint16_t* Ab = buf[kb & 1];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int ks = 2 * kb + s;
+            uint32_t B[16];
+            decode_segment<BITS, CB>(s ? dB : dA, B, k);
+            if (s == 0 && ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dA);
+            if (s == 1 && ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dB);
+            const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
+            const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (t < ntile) {
+                    const uint16_t* arow = Ab + (t * 16 + rr) * kp + s * EXL3C4_KSTEP + 16 * g;
+                    const half8_t Aa = *(const half8_t*)arow, Ac = *(const half8_t*)(arow + 8);
+                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b0, acc[t][0], 0, 0, 0);
+                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b1, acc[t][1], 0, 0, 0);
+                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b2, acc[t][0], 0, 0, 0);
+                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b3, acc[t][1], 0, 0, 0);
+                }
+            }
+        }
+        if (kb + 1 < nb) {
+            stage_store(buf[(kb + 1) & 1], kp, nrows, r);
+        }
+        __syncthreads();
+    }
+}
+
+// gate_up's prefill GEMM: one workgroup per (chunk, 128-column group); xr (prep_gu's rows, sorted-row order) in, the f32
+// sums of the chunk's rows out to part (one split): the epilogue kernel finishes them.
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
+    const int grp = blockIdx.x, chunk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = min(a.plan[0], a.max_chunks);
+    if (chunk >= nch) return;
+    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
+    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const Exl3c4Class& K = a.cls[class_of(a, e)];
+    const int N = K.rows, KC = K.cols;
+    if (grp * 128 >= N) return;
+    const bool up = grp * 128 >= N / 2;
+    float4_t acc[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    pf_gemm<BITS, CB>(a, K, entry_of(a, e), grp * 4 + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows,
+                      up ? KC : 0, lds, acc);
+    const int cc = lane & 15, rg = lane >> 4;
+    const int n = (grp * 4 + wave) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int row = t * 16 + rg * 4 + q;
+            if (row < nrows) {
+                a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
+                a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
+            }
+        }
+}
+
+// down's prefill GEMM: one workgroup per (chunk, 128-column output block); h (rotated, sorted-row order) in; the
+// epilogue (had128, x svh, bf16) in the workgroup through LDS, one row tile at a time. Writes every row of its chunk
+// in its block: a negative sorted_tok and a narrower class's tail as zero; raw sums to dacc.
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
+    const int b = blockIdx.x, chunk = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nch = min(a.plan[0], a.max_chunks);
+    if (chunk >= nch) return;
+    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
+    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const Exl3c4Class& D = a.cls[class_of(a, e)];
+    const int64_t jx = entry_of(a, e);
+    const int N = D.rows;
+    if (b * 128 >= N) {                                           // a narrower class's tail
+        for (int q = wave; q < nrows; q += 4) {
+            uint16_t* out = (uint16_t*)a.y + (int64_t)(row0 + q) * a.y_pitch + b * 128;
+            out[lane] = 0;
+            out[lane + 64] = 0;
+        }
+        return;
+    }
+    float4_t acc[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    pf_gemm<BITS, CB>(a, D, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, lds, acc);
+
+    const void* svh = tab_entry(D.svh, D.svh_stride, jx);
+    const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
+    float* acc_l = (float*)lds;                                   // [16][128], one row tile at a time
+    const int cc = lane & 15, rg = lane >> 4;
+    const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
+    const int ntile = (nrows + 15) >> 4;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {                                 // unrolled: acc[t] stays in registers
+        if (t >= ntile) break;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc_l[(rg * 4 + q) * 128 + col] = acc[t][0][q];
+            acc_l[(rg * 4 + q) * 128 + col + 8] = acc[t][1][q];
+        }
+        __syncthreads();
+        for (int q = wave; q < 16; q += 4) {
+            const int row = t * 16 + q;
+            if (row < nrows) {
+                const int64_t r = row0 + row;
+                float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
+                float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
+                dacc[lane] = y0;
+                dacc[lane + 64] = y1;
+                uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
+                if (a.sorted[r] < 0) {
+                    out[lane] = 0;
+                    out[lane + 64] = 0;
+                } else {
+                    had128_wave(y0, y1, lane);
+                    out[lane] = f2bf(y0 * h2f(sv0));
+                    out[lane + 64] = f2bf(y1 * h2f(sv1));
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // dequant: one wave per block of the stored record; W_hat[n][k] fp16 bits, the radiance [rows, cols] view.
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) void k_dequant(const uint32_t* rec, int rows, int cols, uint16_t* w, int64_t pitch) {
@@ -740,6 +1044,8 @@ template <template <int, int> class F> GemmFn by_bits(int bits, int cb) {
 }
 template <int BITS, int CB> struct GuK { static constexpr GemmFn fn = k_gu<BITS, CB>; };
 template <int BITS, int CB> struct DnK { static constexpr GemmFn fn = k_dn<BITS, CB>; };
+template <int BITS, int CB> struct GuPfK { static constexpr GemmFn fn = k_gu_pf<BITS, CB>; };
+template <int BITS, int CB> struct DnPfK { static constexpr GemmFn fn = k_dn_pf<BITS, CB>; };
 
 template <int BITS> DequantFn dequant_fn(int cb) {
     switch (cb) {
@@ -802,7 +1108,8 @@ extern "C" int exl3c4_dev_gu(const Exl3c4Launch* a, void* stream, void* ev0, voi
 }
 
 extern "C" int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->T * a->nblk;
+    const int per = a->blk_per_wave > 0 ? a->blk_per_wave : 1;
+    const int64_t waves = (int64_t)a->T * ((a->nblk + per - 1) / per);
     if (waves <= 0) return 0;
     return go(k_gepi, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
@@ -813,6 +1120,47 @@ extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, voi
     if (a->nblk <= 0 || a->T <= 0) return 0;
     const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2 + 16 * 128 * 4);
     return go2(f, dim3((unsigned)a->nblk, (unsigned)a->T), (hipStream_t)stream, ev0, ev1, lds, *a);
+}
+
+extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    if (a->T <= 0) return 0;
+    if (ev0 && ev1)
+        hipExtLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0,
+                              *a);
+    else
+        hipLaunchKernelGGL(k_plan, dim3(1), dim3(1024), 0, (hipStream_t)stream, *a);
+    return launched();
+}
+
+extern "C" int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    if (a->T <= 0) return 0;
+    return go(k_rowinfo, (unsigned)((a->T + 255) / 256), (hipStream_t)stream, ev0, ev1, *a);
+}
+
+extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = (int64_t)a->T * a->h_from_gu;
+    if (waves <= 0) return 0;
+    return go(k_rot, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+}
+
+extern "C" int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = a->nblk > 0 ? (int64_t)a->T : 0;
+    if (waves <= 0) return 0;
+    return go(k_zero_dead, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+}
+
+extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
+    if (!f) return EXL3C4_E_DTYPE;
+    if (a->n_grp <= 0 || a->max_chunks <= 0) return 0;
+    return go2(f, dim3((unsigned)a->n_grp, (unsigned)a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
+}
+
+extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemmFn f = by_bits<DnPfK>(a->bits, a->codebook);
+    if (!f) return EXL3C4_E_DTYPE;
+    if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
+    return go2(f, dim3((unsigned)a->nblk, (unsigned)a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

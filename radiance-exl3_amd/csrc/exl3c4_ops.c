@@ -57,39 +57,70 @@ static int log2i(int v) {
     return l;
 }
 
+/* The prefill path serves a launch whose rows average at least this many an expert (T >= n * n_expert): chunks of up
+ * to 64 rows share each decoded weight. Below it the decode kernels (16-row chunks, split-K) serve it. */
+#ifndef EXL3C4_PF_ROWS_PER_EXPERT
+#define EXL3C4_PF_ROWS_PER_EXPERT 8
+#endif
+static int prefill_path(const Exl3c4Op* o, int64_t T) {
+    return o->op != EXL3C4_PREP_GU && T >= EXL3C4_PF_ROWS_PER_EXPERT * o->n_expert;
+}
+
 typedef struct Carve {
-    int64_t row_info, part, dacc, total;
-    int64_t T, part_pitch, dacc_pitch;
+    int     pf;                                   /* the prefill path */
+    int64_t row_info, plan, xr, part, h, dacc, total;
+    int64_t T, part_pitch, dacc_pitch, xr_pitch, h_pitch, max_chunks;
     int     split_gu, gu_lds_pitch, dn_lds_pitch;
 } Carve;
 
-/* The scratch of one launch with T sorted rows, each region 256-B aligned: [row_info | gate_up partial sums | down
- * accumulations]. row_info: the row's owner and chunk rows, written by gate_up's GEMM for the kernels after it. */
+/* The scratch of one launch with T sorted rows, each region 256-B aligned.
+ *   decode path:  [row_info | gate_up split-K partial sums | down accumulations]
+ *   prefill path: [row_info | plan | rotated input | gate_up sums | h (gate_up_down) | down accumulations]
+ * row_info: each row's owner (and, decode path, chunk rows), written by the first kernel for those after it. */
 static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     const int op = o->op;
-    const int64_t rc = max_rows(o);
+    const int64_t rc = max_rows(o), xc = max_cols(o);
     memset(k, 0, sizeof *k);
     k->T = T;
+    k->pf = prefill_path(o, T);
     int64_t off = 0;
     const int gu = op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN;
     const int dn = op == EXL3C4_DOWN || op == EXL3C4_GU_DN;
     k->row_info = off;
-    if (gu) off += ALIGN_UP(T * 8, 256);
+    if (gu || (dn && k->pf)) off += ALIGN_UP(T * 8, 256);
+    k->plan = off;
+    if (k->pf) {
+        k->max_chunks = T / EXL3C4_PF_ROWS + (o->n_expert < T ? o->n_expert : T) + 1;
+        off += ALIGN_UP(16 + 16 * k->max_chunks, 256);
+    }
+    k->xr = off;
+    if (k->pf) {
+        if ((op == EXL3C4_GATE_UP && !o->a_rot) || op == EXL3C4_GU_DN) k->xr_pitch = 2 * xc;
+        else if (op == EXL3C4_DOWN && !o->h_rot) k->xr_pitch = xc;
+        off += ALIGN_UP(T * k->xr_pitch * 2, 256);
+    }
     k->part = off;
     if (gu) {
-        /* split-K: from T and the geometry; at most 12 128-blocks of k a split, so the staged rows fit LDS */
         int64_t nb_min = INT64_MAX, nb_max = 0;
         for (int c = 0; c < o->n_class; ++c) {
             const int64_t nb = o->cls[c].cols / 128;
             if (nb < nb_min) nb_min = nb;
             if (nb > nb_max) nb_max = nb;
         }
-        int s = ksplit_for(chunk_bound(T, o->n_expert), rc / EXL3C4_STRIP, 2 * nb_min);
-        while ((nb_max + s - 1) / s > 12) s *= 2;
+        int s = 1;
+        if (!k->pf) {   /* split-K: from T and the geometry; at most 12 128-blocks of k a split, so rows fit LDS */
+            s = ksplit_for(chunk_bound(T, o->n_expert), rc / EXL3C4_STRIP, 2 * nb_min);
+            while ((nb_max + s - 1) / s > 12) s *= 2;
+            k->gu_lds_pitch = (int)(((nb_max + s - 1) / s) * 128 + 8);
+        }
         k->split_gu = s;
-        k->gu_lds_pitch = (int)(((nb_max + s - 1) / s) * 128 + 8);
         k->part_pitch = rc;
         off += ALIGN_UP(s * T * rc * 4, 256);
+    }
+    k->h = off;
+    if (k->pf && op == EXL3C4_GU_DN) {
+        k->h_pitch = rc / 2;
+        off += ALIGN_UP(T * k->h_pitch * 2, 256);
     }
     k->dacc = off;
     if (dn) {
@@ -234,11 +265,84 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->y = o->y;
     a->y_pitch = o->y_pitch;
     a->y_cols = (int32_t)o->y_cols;
+    a->blk_per_wave = 1;
 }
 
 /* The events of a timed launch go to exactly one kernel of the sequence. */
 typedef struct Timed { int kernel; void *ev0, *ev1; } Timed;
 #define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
+
+/* down's classes: its own, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
+ * (include/exl3_abi.h:751-800; h crosses rotated). */
+static void down_classes(const Exl3c4Op* o, Exl3c4Launch* d) {
+    for (int c = 0; c < o->n_class; ++c) {
+        if (o->op == EXL3C4_GU_DN) {
+            d->cls[c] = o->dn[c];
+            d->cls[c].rows = o->cls[c].cols;
+            d->cls[c].cols = o->cls[c].rows / 2;
+            d->cls[c].suh = o->cls[c].dn_suh;
+            d->cls[c].suh_stride = o->cls[c].dn_suh_stride;
+            d->gcls[c] = o->cls[c];
+        } else {
+            d->cls[c] = o->cls[c];
+        }
+    }
+}
+
+/* The prefill path: plan; the input rotation into scratch (unless the input arrives rotated); gate_up's GEMM and its
+ * epilogue (into y, or into h for gate_up_down); down's GEMM with its epilogue; the rows no run holds zeroed. */
+static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t) {
+    const int op = o->op;
+    int rc;
+    Exl3c4Launch p;
+    base_args(o, k, s, &p);
+    p.row_info = (int32_t*)(s + k->row_info);
+    p.plan = (int32_t*)(s + k->plan);
+    p.max_chunks = (int32_t)k->max_chunks;
+    if ((rc = exl3c4_dev_plan(&p, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
+    if ((rc = exl3c4_dev_rowinfo(&p, stream, NULL, NULL)) != 0) return rc;
+
+    const void* gin = o->x;                       /* gate_up's GEMM input: xr */
+    int64_t gin_pitch = o->x_pitch;
+    const void* din = o->x;                       /* down's GEMM input: h, rotated */
+    int64_t din_pitch = o->x_pitch;
+    if (k->xr_pitch) {
+        Exl3c4Launch r = p;
+        for (int c = 0; c < o->n_class; ++c) r.cls[c] = o->cls[c];
+        r.y = s + k->xr;
+        r.y_pitch = k->xr_pitch;
+        r.h_from_gu = op == EXL3C4_DOWN ? 1 : 2;  /* halves a row */
+        if ((rc = exl3c4_dev_rot(&r, stream, NULL, NULL)) != 0) return rc;
+        if (op == EXL3C4_DOWN) { din = s + k->xr; din_pitch = k->xr_pitch; }
+        else { gin = s + k->xr; gin_pitch = k->xr_pitch; }
+    }
+    if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
+        Exl3c4Launch a = p;
+        for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
+        a.x = gin;
+        a.x_pitch = gin_pitch;
+        a.ksplit = 1;
+        a.n_grp = (int32_t)(max_rows(o) / 128);
+        if ((rc = exl3c4_dev_gu_pf(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
+        a.h_rot = op == EXL3C4_GU_DN ? 1 : o->h_rot;
+        if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
+        else a.nblk = (int32_t)(o->y_cols / 128);
+        a.blk_per_wave = a.nblk;                  /* a wave a row: many rows, no need to spread a row's blocks */
+        if ((rc = exl3c4_dev_gepi(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
+        if (op == EXL3C4_GATE_UP) return EXL3C4_OK;
+        din = s + k->h;
+        din_pitch = k->h_pitch;
+    }
+    Exl3c4Launch d = p;
+    down_classes(o, &d);
+    d.x = din;
+    d.x_pitch = din_pitch;
+    d.nblk = (int32_t)(o->y_cols / 128);
+    d.dacc = (float*)(s + k->dacc);
+    d.dacc_pitch = k->dacc_pitch;
+    if ((rc = exl3c4_dev_dn_pf(&d, stream, EV(EXL3C4_K_DOWN))) != 0) return rc;
+    return exl3c4_dev_zero_dead(&d, stream, NULL, NULL);
+}
 
 /* The launches of each op on the stream -- no planning pass: every workgroup finds its rows' expert itself.
  *   prep_gu       the input rotation
@@ -263,6 +367,8 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
         return exl3c4_dev_prep(&f, stream, EV(EXL3C4_K_PREP));
     }
 
+    if (k.pf) return launch_prefill(o, &k, s, stream, t);
+
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
         base_args(o, &k, s, &a);
@@ -283,18 +389,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
      * (include/exl3_abi.h:751-800; h crosses rotated) */
     Exl3c4Launch d;
     base_args(o, &k, s, &d);
-    for (int c = 0; c < o->n_class; ++c) {
-        if (op == EXL3C4_GU_DN) {
-            d.cls[c] = o->dn[c];
-            d.cls[c].rows = o->cls[c].cols;
-            d.cls[c].cols = o->cls[c].rows / 2;
-            d.cls[c].suh = o->cls[c].dn_suh;
-            d.cls[c].suh_stride = o->cls[c].dn_suh_stride;
-            d.gcls[c] = o->cls[c];
-        } else {
-            d.cls[c] = o->cls[c];
-        }
-    }
+    down_classes(o, &d);
     if (op == EXL3C4_GU_DN) {
         d.h_from_gu = 1;
         d.row_info = (int32_t*)(s + k.row_info);     /* written by gate_up's GEMM */

@@ -154,6 +154,26 @@ def test_ops_four_classes(torch_cuda):
     _check_all(case, "four-class")
 
 
+# ------------------------------------------------------------------------------------------ the prefill path
+# (T >= 8 n_expert rows: chunks of up to 64 rows, a plan, the rotation into scratch, the prefill GEMMs)
+def test_prefill_path_two_classes_several_chunks_with_drops(torch_cuda):
+    case = Case(seed=40, n_tok=96, top_k=2, n_expert=4, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
+                drop=0.1, protect_tail=2, routing="zipf")
+    assert case.T >= 8 * case.n_expert and np.diff(case.off).max() > 64
+    _check_all(case, "prefill two-class")
+
+
+def test_prefill_path_four_classes_mcg(torch_cuda):
+    case = Case(seed=41, n_tok=64, top_k=2, n_expert=8, geoms=[(256, 128), (256, 256), (128, 128), (256, 128)],
+                bits=5, cb="mcg")
+    _check_all(case, "prefill four-class")
+
+
+def test_prefill_path_bf16_3inst(torch_cuda):
+    _check_all(Case(seed=42, n_tok=64, top_k=1, n_expert=2, geoms=[(256, 128)], bits=3, cb="3inst", x_bf16=True),
+               "prefill bf16")
+
+
 @pytest.mark.parametrize("bits", [3, 4, 5])
 @pytest.mark.parametrize("m", [1, 4, 16])
 def test_single_routed_expert_at_the_baseline_geometry(torch_cuda, bits, m):
