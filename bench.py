@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""bench.py -- throughput of the EXL3 routed-expert decode layer on one MI355X.
+"""bench.py -- throughput of the EXL3 routed-expert decode layer on one MI355X; with
+--config 2, 4 or 5 the single expert, the prefill layer or the 48-layer decode stack instead.
 
 One STEP is one routed-MoE layer in decode: 8 tokens (2 sequences x 4 speculative positions) through 512 experts at
 4 bpw (gate/up 2048 -> 2 x 512, down 512 -> 2048, codebook mul1), router softmax -> top-10 -> renormalised, as ONE
@@ -117,6 +118,245 @@ def read_traffic():
         return json.load(f).get("bytes_per_launch")
 
 
+def timed_graph(torch, launch_step, steps, warmup):
+    """Warm up eagerly, capture `steps` steps into one HIP graph, replay once untimed, then time one replay with events
+    around it. Returns ms for the whole replay."""
+    stream = torch.cuda.current_stream()
+    for i in range(warmup):
+        launch_step(i, stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            for i in range(steps):
+                launch_step(i, torch.cuda.current_stream())
+    stream.wait_stream(cap)
+    g.replay()                                    # one untimed replay (first-replay costs)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1)
+
+
+def kernel_ms(torch, exl3c4, ops, scratch, kernel, n):
+    """Average duration (ms) of one kernel of the op sequence over n eager launches, timed by start/stop events
+    around its own dispatch; the launches are queued behind a short spin so that they run back to back."""
+    evs = [(exl3c4.Event(), exl3c4.Event()) for _ in range(n)]
+    stream = torch.cuda.current_stream()
+    torch.cuda._sleep(int(2e6 + 2e5 * n))
+    for i in range(n):
+        rc = exl3c4.launch_timed(ops[i % len(ops)], scratch, kernel, evs[i][0], evs[i][1], stream)
+        if rc:
+            raise RuntimeError(f"timed launch: {exl3c4.STATUS.get(rc, rc)}")
+    torch.cuda.synchronize()
+    return np.array([exl3c4.elapsed_ms(a, b) for a, b in evs])
+
+
+def check_rc(exl3c4, rc):
+    if rc:
+        raise RuntimeError(f"launch: {exl3c4.STATUS.get(rc, rc)}")
+
+
+def common(args, ms, steps, value, unit, workload, extra=None):
+    out = {"metric": "MoE-layer tokens/s + packed-weight GB/s (% HBM peak) decode; prefill % MFMA peak",
+           "value": round(value, 1), "unit": unit, "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+           "ms_per_step": round(ms / steps, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f16", "data": "synthetic", "config": {"workload": workload}}
+    if extra:
+        out["config"].update(extra)
+    return out
+
+
+# ------------------------------------------------------------------------------------------ configs[2]: decode layer
+def run_decode_layer(args, torch, exl3c4):
+    layers = build_layers(torch, args.layers, args.seed)
+    draws = build_draws(torch, args.draws, args.seed + 1)
+    T = M * TOP_K
+    y = torch.zeros((T, H), dtype=torch.int16, device="cuda")
+    ops = []
+    for s in range(max(args.layers, args.draws)):
+        L, D = layers[s % args.layers], draws[s % args.draws]
+        ops.append(exl3c4.make_op(exl3c4.GU_DN, BITS, CB, [L["gu_cls"]], D["x"], D["sorted_tok"], D["off"], y, M,
+                                  TOP_K, dn=[L["dn_cls"]]))
+    scratch = exl3c4.alloc_scratch(ops[0])
+    ms = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch(ops[i % len(ops)], scratch, st)),
+                     args.steps, args.warmup)
+    ms_step = ms / args.steps
+    live = [draws[i % args.draws]["n_live"] for i in range(args.steps)]
+    layer_gbps = float(np.mean(live)) * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
+    durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP, args.steps)
+    gemv_bytes = np.array(live, dtype=np.float64) * GU_CODE_BYTES
+    gemv_gbps = float(np.mean(gemv_bytes) / (np.mean(durs) * 1e-3) / 1e9)
+    cpu = cpu_baseline(draws[0], args.cpu_experts, args.seed + 2) if args.cpu_experts > 0 else None
+    out = common(args, ms, args.steps, M * args.steps / (ms / 1e3), "tokens/s",
+                 "configs[2]: routed MoE layer decode, 512 experts (gate/up 2048->2x512, down 512->2048) at 4 bpw "
+                 "mul1, 8 tokens, router softmax top-10 renormalised, one moe_exl3_gate_up_down launch per step",
+                 {"layers_resident": args.layers, "routing_draws": args.draws,
+                  "mean_live_experts": round(float(np.mean(live)), 2)})
+    out.update({
+        "packed_weight_GBps": round(layer_gbps, 1),
+        "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(),
+                     "kernel": "k_gu<4,mul1> (gate_up GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 3),
+                     "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
+        "cpu_baseline": cpu,
+    })
+    return out
+
+
+# ------------------------------------------------------------------------------------------ configs[1]: one expert
+def run_single_expert(args, torch, exl3c4):
+    """One SwiGLU expert (gate/up 2048 -> 2 x 512, down 512 -> 2048) at K 3, 4, 5 and m 1, 4, 16 tokens, top_k 1: one
+    gate_up_down launch a step; 64 copies of the expert resident, a different one each step (no cache reuse)."""
+    copies, res = 64, []
+    for bits in (3, 4, 5):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(args.seed + bits)
+        gu = torch.randint(0, 256, (copies, 2 * W * H * bits // 8), dtype=torch.uint8, device="cuda", generator=g)
+        dn = torch.randint(0, 256, (copies, H * W * bits // 8), dtype=torch.uint8, device="cuda", generator=g)
+
+        def signs(e, n, mag):
+            s = torch.randint(0, 2, (e, n), device="cuda", generator=g).to(torch.float16) * 2 - 1
+            return (s * mag).contiguous().view(torch.int16)
+        suh, suh1, svh = signs(copies, H, 1.0), signs(copies, H, 1.0), signs(copies, 2 * W, 1 / np.sqrt(H))
+        dsuh, dsvh = signs(copies, W, 1.0), signs(copies, H, 1 / np.sqrt(W))
+        for m in (1, 4, 16):
+            x = torch.randn((m, H), device="cuda", generator=g).to(torch.float16).view(torch.int16)
+            st = torch.arange(m, dtype=torch.int32, device="cuda")
+            offs = []
+            for j in range(copies):        # every row to expert j (of `copies`), the others empty
+                o = np.zeros(copies + 1, np.int32)
+                o[j + 1:] = m
+                offs.append(torch.from_numpy(o).cuda())
+            y = torch.zeros((m, H), dtype=torch.int16, device="cuda")
+            gcls = exl3c4.make_class(2 * W, H, codes=gu, suh=suh, suh1=suh1, svh=svh, dn_suh=dsuh)
+            dcls = exl3c4.make_class(H, W, codes=dn, svh=dsvh)
+            ops = [exl3c4.make_op(exl3c4.GU_DN, bits, CB, [gcls], x, st, offs[j], y, m, 1, dn=[dcls])
+                   for j in range(copies)]
+            scratch = exl3c4.alloc_scratch(ops[0])
+            steps = args.steps
+            ms = timed_graph(torch, lambda i, s_: check_rc(exl3c4, exl3c4.launch(ops[i % copies], scratch, s_)),
+                             steps, args.warmup)
+            us = ms / steps * 1e3
+            byts = 393216 * bits + 15360
+            res.append({"bits": bits, "m": m, "us": round(us, 2), "GBps": round(byts / (us * 1e-6) / 1e9, 1),
+                        "tokens_s": round(m / (us * 1e-6), 1)})
+    k4m16 = [r for r in res if r["bits"] == 4 and r["m"] == 16][0]
+    out = common(args, k4m16["us"] * 1e-3 * args.steps, args.steps, k4m16["tokens_s"], "tokens/s",
+                 "configs[1]: one routed SwiGLU expert (gate/up 2048->2x512, down 512->2048), K 3/4/5, m 1/4/16, "
+                 "top_k 1; value = K=4 m=16", {"cases": res})
+    out["cpu_baseline"] = None
+    return out
+
+
+# ------------------------------------------------------------------------------------------ configs[3]: prefill layer
+def run_prefill_layer(args, torch, exl3c4):
+    import exl3c4_synth as syn
+    layers = build_layers(torch, 2, args.seed)             # two layers alternate (2 x 0.8 GB: no cache reuse)
+    rng = np.random.default_rng(args.seed + 1)
+    n_tok = 2048
+    ids, w = syn.zipf_topk(rng, n_tok, E, TOP_K)
+    st, off = syn.moe_scatter(ids, E)
+    T = st.size
+    x = torch.from_numpy(rng.standard_normal((n_tok, H)).astype(np.float16).view(np.int16)).cuda()
+    stt, offt = torch.from_numpy(st).cuda(), torch.from_numpy(off).cuda()
+    y = torch.zeros((T, H), dtype=torch.int16, device="cuda")
+    ops = [exl3c4.make_op(exl3c4.GU_DN, BITS, CB, [L["gu_cls"]], x, stt, offt, y, n_tok, TOP_K, dn=[L["dn_cls"]])
+           for L in layers]
+    scratch = exl3c4.alloc_scratch(ops[0])
+    steps = max(1, min(args.steps, 40))
+    ms = timed_graph(torch, lambda i, s_: check_rc(exl3c4, exl3c4.launch(ops[i % 2], scratch, s_)), steps,
+                     min(args.warmup, 5))
+    t = ms / steps * 1e-3
+    flops = 2.0 * T * (2 * W * H + H * W)
+    durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP, 10)
+    gu_flops = 2.0 * T * 2 * W * H
+    cnt = np.diff(off)
+    live = int((cnt > 0).sum())
+    out = common(args, ms, steps, n_tok / t, "tokens/s",
+                 "configs[3]: routed MoE layer prefill, 2048 tokens, 512 experts at 4 bpw mul1, Zipf(1.1) "
+                 "Gumbel-top-10 routing, one moe_exl3_gate_up_down launch per step (prefill path)",
+                 {"rows": int(T), "live_experts": live, "max_rows_per_expert": int(cnt.max())})
+    out.update({
+        "mfma_frac": round(flops / t / 2.5e15, 4),
+        "TFLOPs": round(flops / t / 1e12, 1),
+        "packed_weight_GBps": round(live * EXPERT_BYTES / t / 1e9, 1),
+        "roofline": {"bound": "mfma", "achieved": round(gu_flops / (np.mean(durs) * 1e-3) / 1e12, 1),
+                     "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(gu_flops / (np.mean(durs) * 1e-3) / 2.5e15, 4), "traffic": None,
+                     "kernel": "k_gu_pf<4,mul1> (gate_up prefill GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 1),
+                     "flops_per_launch": gu_flops},
+        "cpu_baseline": None,
+    })
+    return out
+
+
+# ------------------------------------------------------------------------------------------ configs[4]: 48 layers
+def run_stack(args, torch, exl3c4):
+    """48 decode layers, all resident, K of gate_up and of down cycling through {2, 3, 4, 6, 8} (gate_up at layer l
+    takes cycle[l % 5], down cycle[(l + 2) % 5]); a layer whose two K agree is one gate_up_down launch, else gate_up
+    (h_rot 1) then down (h_rot 1) through an h buffer. A step is 8 tokens through all the layers, each layer with its
+    own routing draw."""
+    cyc = (2, 3, 4, 6, 8)
+    n_layers = args.stack_layers
+    g = torch.Generator(device="cuda")
+    g.manual_seed(args.seed)
+
+    def signs(n, mag):
+        s = torch.randint(0, 2, (E, n), device="cuda", generator=g).to(torch.float16) * 2 - 1
+        return (s * mag).contiguous().view(torch.int16)
+    draws = build_draws(torch, n_layers, args.seed + 1)
+    T = M * TOP_K
+    y = torch.zeros((T, H), dtype=torch.int16, device="cuda")
+    h = torch.zeros((T, W), dtype=torch.int16, device="cuda")
+    layer_ops, step_bytes, resident = [], 0.0, 0
+    for l in range(n_layers):
+        kg, kd = cyc[l % 5], cyc[(l + 2) % 5]
+        gu = torch.randint(0, 256, (E, 2 * W * H * kg // 8), dtype=torch.uint8, device="cuda", generator=g)
+        dn = torch.randint(0, 256, (E, H * W * kd // 8), dtype=torch.uint8, device="cuda", generator=g)
+        keep = (gu, dn, signs(H, 1.0), signs(H, 1.0), signs(2 * W, 1 / np.sqrt(H)), signs(W, 1.0),
+                signs(H, 1 / np.sqrt(W)))
+        resident += gu.numel() + dn.numel()
+        _, _, suh, suh1, svh, dsuh, dsvh = keep
+        gcls = exl3c4.make_class(2 * W, H, codes=gu, suh=suh, suh1=suh1, svh=svh, dn_suh=dsuh)
+        D = draws[l]
+        if kg == kd:
+            dcls = exl3c4.make_class(H, W, codes=dn, svh=dsvh)
+            ops = [exl3c4.make_op(exl3c4.GU_DN, kg, CB, [gcls], D["x"], D["sorted_tok"], D["off"], y, M, TOP_K,
+                                  dn=[dcls])]
+        else:
+            dcls = exl3c4.make_class(H, W, codes=dn, suh=dsuh, svh=dsvh)
+            ops = [exl3c4.make_op(exl3c4.GATE_UP, kg, CB, [gcls], D["x"], D["sorted_tok"], D["off"], h, M, TOP_K,
+                                  h_rot=1, a_rot=0),
+                   exl3c4.make_op(exl3c4.DOWN, kd, CB, [dcls], h, D["sorted_tok"], D["off"], y, M, TOP_K, h_rot=1)]
+        layer_ops.append((ops, keep))
+        step_bytes += D["n_live"] * (2 * W * H * kg // 8 + H * W * kd // 8 + 2 * (H + H + 2 * W) + 2 * (W + H))
+    scratch = torch.empty(max(exl3c4.scratch_bytes(o) for ops, _ in layer_ops for o in ops), dtype=torch.uint8,
+                          device="cuda")
+
+    def step(i, st):
+        for ops, _ in layer_ops:
+            for o in ops:
+                check_rc(exl3c4, exl3c4.launch(o, scratch, st))
+    steps = max(1, min(args.steps, 20))
+    ms = timed_graph(torch, step, steps, min(args.warmup, 3))
+    t = ms / steps * 1e-3
+    out = common(args, ms, steps, M / t, "tokens/s",
+                 f"configs[4]: {n_layers} routed MoE decode layers resident, gate_up / down K cycling "
+                 "{2,3,4,6,8} per projection, 8 tokens, per-layer softmax top-10 routing; one step = all layers",
+                 {"layers": n_layers, "resident_codes_GB": round(resident / 1e9, 2),
+                  "step_packed_bytes": int(step_bytes)})
+    out.update({"packed_weight_GBps": round(step_bytes / t / 1e9, 1),
+                "hbm_frac": round(step_bytes / t / 1e9 / HBM_PEAK_GBPS, 4), "roofline": None, "cpu_baseline": None})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,6 +366,10 @@ def main():
     ap.add_argument("--draws", type=int, default=8)
     ap.add_argument("--cpu-experts", type=int, default=24, help="live experts in the CPU-baseline sample (0: skip)")
     ap.add_argument("--seed", type=int, default=20261013)
+    ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5),
+                    help="BASELINE.json configs[n-1]: 2 one expert, 3 decode layer (default), 4 prefill layer, "
+                         "5 48-layer decode stack")
+    ap.add_argument("--stack-layers", type=int, default=48)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 20 plain device-to-device copies of BYTES (the HBM-counter calibration) and exit")
     args = ap.parse_args()
@@ -146,98 +390,8 @@ def main():
     import exl3c4
     exl3c4.lib()
     torch.cuda.set_device(0)
-    layers = build_layers(torch, args.layers, args.seed)
-    draws = build_draws(torch, args.draws, args.seed + 1)
-    T = M * TOP_K
-    y = torch.zeros((T, H), dtype=torch.int16, device="cuda")
-    ops = []
-    for s in range(max(args.layers, args.draws)):
-        L, D = layers[s % args.layers], draws[s % args.draws]
-        ops.append(exl3c4.make_op(exl3c4.GU_DN, BITS, CB, [L["gu_cls"]], D["x"], D["sorted_tok"], D["off"], y, M,
-                                  TOP_K, dn=[L["dn_cls"]]))
-    scratch = exl3c4.alloc_scratch(ops[0])
-    stream = torch.cuda.current_stream()
-
-    def step(i):
-        rc = exl3c4.launch(ops[i % len(ops)], scratch, stream)
-        if rc:
-            raise RuntimeError(f"launch: {exl3c4.STATUS.get(rc, rc)}")
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # the timed region: K steps captured once as a HIP graph, replayed
-    g = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(g, stream=cap):
-            for i in range(args.steps):
-                rc = exl3c4.launch(ops[i % len(ops)], scratch, torch.cuda.current_stream())
-                if rc:
-                    raise RuntimeError(f"launch under capture: {exl3c4.STATUS.get(rc, rc)}")
-    stream.wait_stream(cap)
-    g.replay()                                    # one untimed replay (first-replay costs)
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1)
-    ms_step = ms / args.steps
-    tokens_s = M * args.steps / (ms / 1e3)
-    live = [draws[i % args.draws]["n_live"] for i in range(args.steps)]
-    layer_bytes = float(np.mean(live)) * EXPERT_BYTES
-    layer_gbps = layer_bytes / (ms_step * 1e-3) / 1e9
-
-    # the dominant kernel (gate_up's GEMM), live: events stamped around its own dispatch, eager steps queued behind a
-    # short spin so that they run back to back as in the timed region (no host gaps between them)
-    evs = [(exl3c4.Event(), exl3c4.Event()) for _ in range(args.steps)]
-    torch.cuda._sleep(int(2e6 + 2e5 * args.steps))
-    for i in range(args.steps):
-        a, b = evs[i]
-        rc = exl3c4.launch_timed(ops[i % len(ops)], scratch, exl3c4.K_GATE_UP, a, b, stream)
-        if rc:
-            raise RuntimeError(f"timed launch: {exl3c4.STATUS.get(rc, rc)}")
-    torch.cuda.synchronize()
-    durs = np.array([exl3c4.elapsed_ms(a, b) for a, b in evs])      # ms
-    gemv_bytes = np.array(live, dtype=np.float64) * GU_CODE_BYTES
-    gemv_gbps = float(np.mean(gemv_bytes) / (np.mean(durs) * 1e-3) / 1e9)
-
-    cpu = None
-    if args.cpu_experts > 0:
-        cpu = cpu_baseline(draws[0], args.cpu_experts, args.seed + 2)
-
-    out = {
-        "metric": "MoE-layer tokens/s + packed-weight GB/s (% HBM peak) decode; prefill % MFMA peak",
-        "value": round(tokens_s, 1),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic",
-        "config": {"workload": "configs[2]: routed MoE layer decode, 512 experts (gate/up 2048->2x512, down "
-                               "512->2048) at 4 bpw mul1, 8 tokens, router softmax top-10 renormalised, one "
-                               "moe_exl3_gate_up_down launch per step",
-                   "layers_resident": args.layers, "routing_draws": args.draws,
-                   "mean_live_experts": round(float(np.mean(live)), 2)},
-        "packed_weight_GBps": round(layer_gbps, 1),
-        "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(),
-                     "kernel": "k_gu<4,mul1> (gate_up GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 3),
-                     "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(out), flush=True)
+    run = {2: run_single_expert, 3: run_decode_layer, 4: run_prefill_layer, 5: run_stack}[args.config]
+    print(json.dumps(run(args, torch, exl3c4)), flush=True)
 
 
 if __name__ == "__main__":

@@ -57,13 +57,14 @@ static int log2i(int v) {
     return l;
 }
 
-/* The prefill path serves a launch whose rows average at least this many an expert (T >= n * n_expert): chunks of up
- * to 64 rows share each decoded weight. Below it the decode kernels (16-row chunks, split-K) serve it. */
+/* The prefill path serves a launch of at least 64 rows whose rows average at least this many an expert
+ * (T >= n * n_expert): chunks of up to 64 rows share each decoded weight, over seven launches. Below it the decode
+ * kernels (16-row chunks, split-K, two launches) serve it. A function of T and n_expert only (never of the routing). */
 #ifndef EXL3C4_PF_ROWS_PER_EXPERT
 #define EXL3C4_PF_ROWS_PER_EXPERT 8
 #endif
 static int prefill_path(const Exl3c4Op* o, int64_t T) {
-    return o->op != EXL3C4_PREP_GU && T >= EXL3C4_PF_ROWS_PER_EXPERT * o->n_expert;
+    return o->op != EXL3C4_PREP_GU && T >= 64 && T >= EXL3C4_PF_ROWS_PER_EXPERT * o->n_expert;
 }
 
 typedef struct Carve {
