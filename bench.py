@@ -35,6 +35,7 @@ import numpy as np
 H, W, E, TOP_K, M, BITS, CB = 2048, 512, 512, 10, 8, 4, "mul1"
 HBM_PEAK_GBPS = 8000.0
 GU_CODE_BYTES = 2 * W * H * BITS // 8            # one expert's gate_up codes (the GEMV's weight stream)
+CODE_BYTES = 3 * W * H * BITS // 8               # one expert's gate_up and down codes
 EXPERT_BYTES = 3 * W * H * BITS // 8 + 2 * (H + H + 2 * W) + 2 * (W + H)   # codes + scale planes: 1,588,224 at K=4
 
 
@@ -109,9 +110,10 @@ def cpu_baseline(draw, max_experts, seed):
                        f"to the whole layer")}
 
 
-def read_traffic():
-    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary, if there is one."""
-    p = os.path.join(ROOT, "profiles", "traffic_k_gu_decode.json")
+def read_traffic(name):
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3 --pmc summary
+    (profiles/traffic_<name>.json), if there is one."""
+    p = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -188,10 +190,15 @@ def run_decode_layer(args, torch, exl3c4):
                      args.steps, args.warmup)
     ms_step = ms / args.steps
     live = [draws[i % args.draws]["n_live"] for i in range(args.steps)]
+    st = exl3c4.launch_status(ops[0], scratch)
+    if st:
+        raise RuntimeError(f"gate_up_down's single kernel left status {st}")
     layer_gbps = float(np.mean(live)) * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
-    durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP, args.steps)
-    gemv_bytes = np.array(live, dtype=np.float64) * GU_CODE_BYTES
+    one = T >= exl3c4.GD_FUSE_MIN_T           # gate_up_down runs as one kernel: that kernel is the one timed
+    durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP_DOWN if one else exl3c4.K_GATE_UP, args.steps)
+    gemv_bytes = np.array(live, dtype=np.float64) * (CODE_BYTES if one else GU_CODE_BYTES)
     gemv_gbps = float(np.mean(gemv_bytes) / (np.mean(durs) * 1e-3) / 1e9)
+    kname = "k_gd_decode" if one else "k_gu_decode"
     cpu = cpu_baseline(draws[0], args.cpu_experts, args.seed + 2) if args.cpu_experts > 0 else None
     out = common(args, ms, args.steps, M * args.steps / (ms / 1e3), "tokens/s",
                  "configs[2]: routed MoE layer decode, 512 experts (gate/up 2048->2x512, down 512->2048) at 4 bpw "
@@ -202,8 +209,9 @@ def run_decode_layer(args, torch, exl3c4):
         "packed_weight_GBps": round(layer_gbps, 1),
         "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(),
-                     "kernel": "k_gu<4,mul1> (gate_up GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 3),
+                     "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(kname),
+                     "kernel": "k_gd<4,mul1> (gate_up_down, one kernel)" if one else "k_gu<4,mul1> (gate_up GEMM)",
+                     "avg_us": round(float(np.mean(durs)) * 1e3, 3),
                      "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
         "cpu_baseline": cpu,
     })

@@ -114,8 +114,11 @@ int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* ro
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
 /* The kernels a launch can run: prep_gu's rotation; gate_up's GEMM (with its input rotation), then for gate_up alone
- * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums). */
-enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3 };
+ * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums); and
+ * gate_up_down's single kernel, which runs both GEMMs in one dispatch at decode once T >= EXL3C4_GD_FUSE_MIN_T.
+ * exl3c4_launch_timed refuses (EXL3C4_E_INVAL) a kernel that the launch does not run. */
+enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3, EXL3C4_K_GATE_UP_DOWN = 4 };
+#define EXL3C4_GD_FUSE_MIN_T 32
 
 /* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and
  * ev_stop (two hipEvent_t the caller created) at its start and end: the duration of that one kernel, read with
@@ -131,6 +134,12 @@ int exl3c4_launch_timed(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes
  * of the accumulation itself (the values before any narrowing); no counterpart in the reference. */
 int exl3c4_scratch_partials(const Exl3c4Op* op, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,
                             int32_t* splits);
+
+/* Where a launch of `op` that runs gate_up_down's single kernel leaves its status word in its scratch (an int32 at
+ * scratch + *offset): 0 after a good launch; 1 when a down unit's wait for its row's gate_up units gave up (after
+ * 0.5 s), and the output is then void. EXL3C4_E_INVAL when the launch does not run that kernel. A checker's entry;
+ * no counterpart in the reference. */
+int exl3c4_scratch_status(const Exl3c4Op* op, int64_t* offset);
 
 /* W_hat of one stored weight [rows, cols] as fp16 bits [rows][w_pitch] on the device -- the same decode the GEMMs run,
  * exposed so it can be compared bit for bit with common/exl3_decode.c:193-221. bits 1..8 (K = 1 is decoder-only,

@@ -17,6 +17,8 @@ extern "C" {
 /* Columns one wave's strip holds (two 16-column tiles) and k one step consumes (four 16-k tiles). */
 #define EXL3C4_STRIP 32
 #define EXL3C4_KSTEP 64
+/* int32 words between two row counters of gate_up_down's single kernel (256 B: each counter its own cache line) */
+#define EXL3C4_SYNC_STRIDE 64
 /* Rows of one chunk on the prefill path (four MFMA row tiles decode-shared). */
 #define EXL3C4_PF_ROWS 64
 
@@ -48,6 +50,10 @@ typedef struct Exl3c4Launch {
     int32_t*       plan;          /* prefill: [0] chunk count, then int4 {expert, row0, rows, 0} per chunk */
     int32_t        max_chunks;
     int32_t        blk_per_wave;  /* gate_up's epilogue: 128-blocks of a row one wave takes */
+    int32_t        lds_pitch_gu;  /* gate_up_down in one launch: gate_up's staged row pitch (lds_pitch is down's) */
+    int32_t*       sync;          /* gate_up_down in one launch: a status word, then row i's counter at (i + 1) * SYNC_STRIDE */
+    uint16_t*      hbuf;          /* gate_up_down in one launch: h (rotated, f16) of every chunk's rows [T][hbuf_pitch] */
+    int64_t        hbuf_pitch;
 } Exl3c4Launch;
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the
@@ -56,6 +62,9 @@ int exl3c4_dev_prep(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gu(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+/* gate_up_down in one launch (k_gd): sync[0..T] zeroed first (exl3c4_dev_fill), then gate_up and down units */
+int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream);
 /* the prefill path */
 int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);

@@ -371,8 +371,21 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
 
 __device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
 
+// A partial sum as gate_up_down's single kernel exchanges it between workgroups: a relaxed atomic access at agent
+// scope, coherent across the XCDs' L2 caches by itself (ordered by the row counter: the writer waits for its stores
+// before it counts, the reader reads after the count is whole).
+template <bool COH> __device__ __forceinline__ float part_ld(const __attribute__((address_space(1))) float* p) {
+    if (COH) return __hip_atomic_load((const float*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+template <bool COH> __device__ __forceinline__ void part_st(float* p, float v) {
+    if (COH) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+
 // The split-K partial sums of four columns of sorted row i, added in ascending split order (the order fixes the
 // bits). The loads go out four splits at a time (16 registers), so S / 4 round trips in all.
+template <bool COH>
 __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, const int (&col)[4], float (&out)[4]) {
     const __attribute__((address_space(1))) float* p =
         (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
@@ -382,8 +395,8 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
         float v[4][2];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            v[c][0] = p[col[c]];
-            v[c][1] = S == 2 ? p[st + col[c]] : 0.f;
+            v[c][0] = part_ld<COH>(p + col[c]);
+            v[c][1] = S == 2 ? part_ld<COH>(p + st + col[c]) : 0.f;
         }
 #pragma unroll
         for (int c = 0; c < 4; ++c) out[c] = S == 2 ? v[c][0] + v[c][1] : v[c][0];
@@ -394,7 +407,7 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) v[c][q] = p[(int64_t)(q0 + q) * st + col[c]];
+            for (int c = 0; c < 4; ++c) v[c][q] = part_ld<COH>(p + (int64_t)(q0 + q) * st + col[c]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float t = q0 == 0 ? v[c][0] : out[c] + v[c][0];
@@ -409,6 +422,7 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
 // sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
 // values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
 // 187-212).
+template <bool COH>
 __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
                                               int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
     const void* svh = tab_entry(K.svh, K.svh_stride, jx);
@@ -419,7 +433,7 @@ __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c
     const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
     const int col[4] = { n0, n1, width + n0, width + n1 };
     float acc[4];
-    sum_splits4(a, i, col, acc);
+    sum_splits4<COH>(a, i, col, acc);
     float g0 = acc[0], g1 = acc[1], u0 = acc[2], u1 = acc[3];
     had128_wave(g0, g1, lane);
     had128_wave(u0, u1, lane);
@@ -456,17 +470,33 @@ __device__ __forceinline__ void mma_step(const uint32_t (&d)[BITS], const uint16
     acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
 }
 
-// The wave's strip over `ksn` steps (even, or 0) of its stream `rec`, whose first two steps' words are already in dA /
-// dB, against the rows staged in LDS; two steps of words in flight while one is decoded.
+// The codes of the next PF steps of a wave's stream: in flight while the earlier steps are decoded.
+#ifndef EXL3C4_GEMV_PF
+#define EXL3C4_GEMV_PF 2
+#endif
+template <int BITS> struct CodeRing { uint32_t d[EXL3C4_GEMV_PF][BITS]; };
+
+template <int BITS> __device__ __forceinline__ void prime(gu32p rec, int ksn, CodeRing<BITS>& r) {
+#pragma unroll
+    for (int q = 0; q < EXL3C4_GEMV_PF; ++q)
+        if (q < ksn) load_words<BITS>(rec + q * 64 * BITS, r.d[q]);
+}
+
+// The wave's strip over `ksn` steps of its stream `rec`, whose first steps' words are already in flight in `r`
+// (prime), against the rows staged in LDS.
 template <int BITS, int CB>
-__device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, uint32_t (&dA)[BITS], uint32_t (&dB)[BITS],
-                                           const uint16_t* arow, float4_t& acc0, float4_t& acc1) {
+__device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r, const uint16_t* arow,
+                                           float4_t& acc0, float4_t& acc1) {
     const Mul1Consts k = mul1_consts();
-    for (int s = 0; s < ksn; s += 2) {
-        mma_step<BITS, CB>(dA, arow + s * EXL3C4_KSTEP, k, acc0, acc1);
-        if (s + 2 < ksn) load_words<BITS>(rec + (s + 2) * 64 * BITS, dA);
-        mma_step<BITS, CB>(dB, arow + (s + 1) * EXL3C4_KSTEP, k, acc0, acc1);
-        if (s + 3 < ksn) load_words<BITS>(rec + (s + 3) * 64 * BITS, dB);
+    constexpr int PF = EXL3C4_GEMV_PF;
+    for (int s = 0; s < ksn; s += PF) {
+#pragma unroll
+        for (int q = 0; q < PF; ++q) {
+            if (s + q < ksn) {
+                mma_step<BITS, CB>(r.d[q], arow + (s + q) * EXL3C4_KSTEP, k, acc0, acc1);
+                if (s + q + PF < ksn) load_words<BITS>(rec + (s + q + PF) * 64 * BITS, r.d[q]);
+            }
+        }
     }
 }
 
@@ -475,26 +505,27 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, uint32_t (&dA)[BI
 // strips over the split's 128-blocks of k; the split's input rows -- rotated here, f16(had128(f16(x * suh or suh1)))
 // of the token's row, or read as given (a_rot) -- are staged once in LDS for all four. The strip's sums go to
 // part[split][row][col]; their consumer adds the splits in a fixed order, so the bits do not depend on scheduling.
-// Workgroup x = 0 of each row records the row's owner and chunk rows in row_info for the kernels that follow.
-template <int BITS, int CB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_gu(const Exl3c4Launch a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    const int i = blockIdx.y;
+// Unit u = group u >> ksplit_log2, split u & (S - 1) of row i; kp: halves a staged row. Returns the chunk's rows (0 when
+// row i starts none) and the row's owner. In its own kernel (k_gu) unit 0 of each row records the row's owner and chunk rows in row_info
+// for the kernels that follow; inside gate_up_down's single launch (FUSED) the classes are gcls.
+struct GuRows { int nrows, e; };
+template <int BITS, int CB, bool FUSED>
+__device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, int kp, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int S = a.ksplit;
-    const int grp = (int)(blockIdx.x >> a.ksplit_log2), split = (int)(blockIdx.x & (S - 1));
+    const int grp = u >> a.ksplit_log2, split = u & (S - 1);
     const Owner w = owner_wg(a, i);
     const int nrows = chunk_rows(w, i);
-    if (blockIdx.x == 0 && threadIdx.x == 0) {
+    if (!FUSED && u == 0 && threadIdx.x == 0) {
         a.row_info[2 * i] = w.e;
         a.row_info[2 * i + 1] = nrows;
     }
-    if (nrows == 0) return;
+    if (nrows == 0) return GuRows{ 0, w.e };
     const int c = class_of(a, w.e);
     const int64_t jx = entry_of(a, w.e);
-    const Exl3c4Class& K = a.cls[c];
+    const Exl3c4Class& K = FUSED ? a.gcls[c] : a.cls[c];
     const int N = K.rows, KC = K.cols;
-    if (grp * 128 >= N) return;
+    if (grp * 128 >= N) return GuRows{ nrows, w.e };
     const int strip = grp * 4 + wave;
     const bool up = grp * 128 >= N / 2;
     const int nb = KC / 128, per = (nb + S - 1) / S;
@@ -502,13 +533,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     const int ksn = 2 * (b1 - b0);
     const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_stride, jx) +
                       ((int64_t)strip * (KC / EXL3C4_KSTEP) + 2 * b0) * 64 * BITS + lane * BITS;
-    uint32_t dA[BITS], dB[BITS];
-    if (ksn > 0) {                                                // its first two steps' words fly during the staging
-        load_words<BITS>(rec, dA);
-        load_words<BITS>(rec + 64 * BITS, dB);
-    }
+    CodeRing<BITS> ring;
+    prime<BITS>(rec, ksn, ring);                                  // its first steps' words fly during the staging
 
-    const int kp = a.lds_pitch;
     uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
     const void* sv = up ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
     for (int q = 0; q < nrows; ++q) {
@@ -535,7 +562,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     __syncthreads();
 
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    gemv_strip<BITS, CB>(rec, ksn, dA, dB, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
+    gemv_strip<BITS, CB>(rec, ksn, ring, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // D lane l: column l % 16 (c' = 2 s + t -> weight row 32 nb + 16 t + s, + 8 for acc1), rows 4 (l / 16) + 0..3
     const int cc = lane & 15, rg = lane >> 4;
@@ -545,10 +572,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
     for (int q = 0; q < 4; ++q) {
         const int tok = rg * 4 + q;
         if (tok < nrows) {
-            pp[(int64_t)(i + tok) * a.part_pitch + n] = acc0[q];
-            pp[(int64_t)(i + tok) * a.part_pitch + n + 8] = acc1[q];
+            part_st<FUSED>(pp + (int64_t)(i + tok) * a.part_pitch + n, acc0[q]);
+            part_st<FUSED>(pp + (int64_t)(i + tok) * a.part_pitch + n + 8, acc1[q]);
         }
     }
+    return GuRows{ nrows, w.e };
+}
+
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) void k_gu(const Exl3c4Launch a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    gu_unit<BITS, CB, false>(a, blockIdx.y, blockIdx.x, a.lds_pitch, lds);
 }
 
 // gate_up's epilogue (gate_up alone): one wave per (sorted row i, 128-column block b) of h, from the partial sums.
@@ -566,10 +600,38 @@ __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
     for (int b = b0; b < b1; ++b) {
         uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
         uint16_t v0 = 0, v1 = 0;
-        if (!dead && b * 128 < a.cls[c].rows / 2) gate_up_block(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
+        if (!dead && b * 128 < a.cls[c].rows / 2)
+            gate_up_block<false>(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
         out[lane] = v0;
         out[lane + 64] = v1;
     }
+}
+
+// Row i's counter: each in its own cache line, so that polls and counts of different rows do not meet.
+__device__ __forceinline__ int32_t* row_counter(const Exl3c4Launch& a, int i) {
+    return a.sync + (int64_t)(i + 1) * EXL3C4_SYNC_STRIDE;
+}
+
+// A down unit of gate_up_down's single launch waits here until its chunk's h is stored: row i's counter reaches
+// n_grp x ksplit + 1 (one count per gate_up unit of row i once its sums are stored, one more once the last of them has
+// formed h). The wait gives up after EXL3C4_WAIT_TICKS of the 100 MHz clock, or soon after another workgroup gave up,
+// and sets bit 0 of the status word sync[0] (the output is then void; the launch still ends).
+#define EXL3C4_WAIT_TICKS 50000000ull
+__device__ __forceinline__ void wait_gate_up(const Exl3c4Launch& a, int i) {
+    if (threadIdx.x == 0) {
+        const int want = (a.n_grp << a.ksplit_log2) + 1;
+        const int32_t* cnt = row_counter(a, i);
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        for (unsigned n = 1; __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want; ++n) {
+            __builtin_amdgcn_s_sleep(8);
+            if ((n & 15) == 0 && ((__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1) ||
+                                  __builtin_amdgcn_s_memrealtime() - t0 > EXL3C4_WAIT_TICKS)) {
+                __hip_atomic_fetch_or(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
 }
 
 // down, one workgroup per (sorted row i, 128-column output block b); the workgroup keyed on a chunk's first row takes
@@ -578,14 +640,13 @@ __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
 // first: gate_up's h_rot = 1 output computed from gate_up's partial sums (gate_up_down), or the rows of x, rotated
 // (h_rot = 0) or as given (down alone). The raw accumulations also go to `dacc` (a checker's view of the sums before
 // any narrowing). Every (row, block) of y is written once: a row no run holds, a negative sorted_tok and a narrower
-// class's tail as zero.
-template <int BITS, int CB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_dn(const Exl3c4Launch a) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    const int b = blockIdx.x, i = blockIdx.y;
+// class's tail as zero. Inside gate_up_down's single launch (FUSED) the workgroup finds the row's owner itself and
+// waits for the row's gate_up units before it reads their sums.
+template <int BITS, int CB, bool FUSED>
+__device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int e, nrows;
-    if (a.row_info) {
+    if (!FUSED && a.row_info) {
         e = a.row_info[2 * i];
         nrows = a.row_info[2 * i + 1];
     } else {
@@ -616,18 +677,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     }
     const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
     uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
-    float* acc_l = (float*)(lds + 16 * kp * 2);                   // [16][128]
+    float* acc_l = (float*)lds;                                   // [16][128], over A once every wave is done with it
 
     // this wave's strip of the block, all of k; its first codes are in flight while the rows are staged
     const int strip = 4 * b + wave;
     const int ksteps = KC / EXL3C4_KSTEP;
     const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
-    uint32_t dA[BITS], dB[BITS];
-    load_words<BITS>(rec, dA);
-    load_words<BITS>(rec + 64 * BITS, dB);                       // k is at least 128: two steps
+    CodeRing<BITS> ring;
+    prime<BITS>(rec, ksteps, ring);
     const void* svh = tab_entry(D.svh, D.svh_stride, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_stride, jx) : nullptr;
+    if (FUSED) wait_gate_up(a, i);
 
     // stage the chunk's rows
     const int nhb = KC / 128;
@@ -635,8 +696,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
         const int64_t r = i + q;
         for (int hb = wave; hb < nhb; hb += 4) {
             uint16_t v0 = 0, v1 = 0;
-            if (a.h_from_gu) {
-                if (a.sorted[r] >= 0) gate_up_block(a, a.gcls[c], r, hb, jx, 1, lane, v0, v1);
+            if (FUSED) {                                          // the row's h, formed once (row_h)
+                const uint16_t* hs = a.hbuf + r * a.hbuf_pitch + hb * 128;
+                v0 = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v1 = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else if (a.h_from_gu) {
+                if (a.sorted[r] >= 0) gate_up_block<false>(a, a.gcls[c], r, hb, jx, 1, lane, v0, v1);
             } else {
                 const void* xs = (const uint16_t*)a.x + r * a.x_pitch + hb * 128;
                 const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
@@ -654,9 +719,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     __syncthreads();
 
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    gemv_strip<BITS, CB>(rec, ksteps, dA, dB, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
+    gemv_strip<BITS, CB>(rec, ksteps, ring, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // the block's accumulations to LDS (column of D lane l: 16 (l & 1) + (l / 2) within the strip, + 8 for acc1)
+    __syncthreads();
     const int cc = lane & 15, rg = lane >> 4;
     const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
 #pragma unroll
@@ -685,6 +751,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
         out[lane] = f2bf(y0 * h2f(sv0));
         out[lane + 64] = f2bf(y1 * h2f(sv1));
     }
+}
+
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_dn(const Exl3c4Launch a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    dn_unit<BITS, CB, false>(a, blockIdx.x, blockIdx.y, lds);
+}
+
+// h of a chunk's rows (gate_up's epilogue with h_rot: had128, x svh, f16(silu(gate) * up), f16(had(f16(h * dn_suh))))
+// from the rows' partial sums, once, by the row's last gate_up unit: into hbuf, then one more count on row i's counter.
+__device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows& g) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = class_of(a, g.e);
+    const int64_t jx = entry_of(a, g.e);
+    const Exl3c4Class& G = a.gcls[c];
+    const int nhb = G.rows / 256;                                  // h's 128-blocks: (rows / 2) / 128
+    for (int t = wave; t < g.nrows * nhb; t += 4) {
+        const int q = t / nhb, hb = t - q * nhb;
+        const int64_t r = i + q;
+        uint16_t v0 = 0, v1 = 0;
+        if (a.sorted[r] >= 0) gate_up_block<true>(a, G, r, hb, jx, 1, lane, v0, v1);
+        uint16_t* h = a.hbuf + r * a.hbuf_pitch + hb * 128;
+        __hip_atomic_store(h + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(h + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, i), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// gate_up_down in one launch (decode path). Workgroups g = 8 k + x (x < 8) take the sorted rows i = x (mod 8): first
+// every gate_up unit of those rows (row-major, the n_grp x ksplit units of k_gu), then every down unit (row-major, the
+// nblk blocks of k_dn). A gate_up unit of a chunk's row adds one to its counter once its sums are stored, and the last of
+// them forms the chunk's h (row_h) and adds one more; a down unit of that row waits for n_grp x ksplit + 1. The dispatcher deals workgroups to the 8 XCDs in turn and each XCD starts its
+// workgroups in order, so the workgroups g = x (mod 8) share one XCD (its L2 holds the row's sums) and when a down unit
+// runs, every gate_up unit before it has started; gate_up units never wait, so the waits end. The sums cross as
+// coherent accesses (part_ld / part_st), so the bits do not depend on where a workgroup lands.
+template <int BITS, int CB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_gd(const Exl3c4Launch a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
+    const int rows = xcd < a.T ? (a.T - 1 - xcd) / 8 + 1 : 0;
+    const int ugu = a.n_grp << a.ksplit_log2;
+    if (slot < rows * ugu) {
+        const int i = xcd + 8 * (slot / ugu);
+        const GuRows g = gu_unit<BITS, CB, true>(a, i, slot % ugu, a.lds_pitch_gu, lds);
+        if (g.nrows > 0) {
+            __shared__ int last_s;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // this thread's sums are stored
+            __syncthreads();
+            if (threadIdx.x == 0)
+                last_s = __hip_atomic_fetch_add(row_counter(a, i), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         ugu - 1;
+            __syncthreads();
+            if (last_s) row_h(a, i, g);                                // the row's last gate_up unit forms h
+        }
+        return;
+    }
+    const int d = slot - rows * ugu;
+    if (d < rows * a.nblk) dn_unit<BITS, CB, true>(a, d % a.nblk, xcd + 8 * (d / a.nblk), lds);
+}
+
+__global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j < n) p[j] = 0;
 }
 
 // ------------------------------------------------------------------------------------------------ the prefill path
@@ -1044,6 +1175,7 @@ template <template <int, int> class F> GemmFn by_bits(int bits, int cb) {
 }
 template <int BITS, int CB> struct GuK { static constexpr GemmFn fn = k_gu<BITS, CB>; };
 template <int BITS, int CB> struct DnK { static constexpr GemmFn fn = k_dn<BITS, CB>; };
+template <int BITS, int CB> struct GdK { static constexpr GemmFn fn = k_gd<BITS, CB>; };
 template <int BITS, int CB> struct GuPfK { static constexpr GemmFn fn = k_gu_pf<BITS, CB>; };
 template <int BITS, int CB> struct DnPfK { static constexpr GemmFn fn = k_dn_pf<BITS, CB>; };
 
@@ -1091,6 +1223,12 @@ int go2(F f, dim3 grid, hipStream_t s, void* ev0, void* ev1, uint32_t lds, Args.
     return hipGetLastError() == hipSuccess ? 0 : EXL3C4_E_DEVICE;
 }
 
+// down's LDS: the staged rows [16][lds_pitch] halves, later the block's accumulations [16][128] f32 over them
+uint32_t dn_lds_bytes(const Exl3c4Launch* a) {
+    const uint32_t rows = (uint32_t)(16 * a->lds_pitch * 2), acc = 16 * 128 * 4;
+    return rows > acc ? rows : acc;
+}
+
 }  // namespace
 
 extern "C" int exl3c4_dev_prep(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
@@ -1118,8 +1256,22 @@ extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, voi
     const GemmFn f = by_bits<DnK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->T <= 0) return 0;
-    const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2 + 16 * 128 * 4);
-    return go2(f, dim3((unsigned)a->nblk, (unsigned)a->T), (hipStream_t)stream, ev0, ev1, lds, *a);
+    return go2(f, dim3((unsigned)a->nblk, (unsigned)a->T), (hipStream_t)stream, ev0, ev1, dn_lds_bytes(a), *a);
+}
+
+extern "C" int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const GemmFn f = by_bits<GdK>(a->bits, a->codebook);
+    if (!f) return EXL3C4_E_DTYPE;
+    if (a->T <= 0 || a->n_grp <= 0 || a->nblk <= 0) return 0;
+    const uint32_t gu_lds = (uint32_t)(16 * a->lds_pitch_gu * 2), dn_lds = dn_lds_bytes(a);
+    const int64_t per_xcd = (int64_t)((a->T + 7) / 8) * (((int64_t)a->n_grp << a->ksplit_log2) + a->nblk);
+    return go2(f, dim3((unsigned)(8 * per_xcd)), (hipStream_t)stream, ev0, ev1, gu_lds > dn_lds ? gu_lds : dn_lds, *a);
+}
+
+extern "C" int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(k_fill, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, p, n);
+    return launched();
 }
 
 extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {

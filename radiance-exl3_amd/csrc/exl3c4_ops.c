@@ -67,15 +67,23 @@ static int prefill_path(const Exl3c4Op* o, int64_t T) {
     return o->op != EXL3C4_PREP_GU && T >= 64 && T >= EXL3C4_PF_ROWS_PER_EXPERT * o->n_expert;
 }
 
+/* gate_up_down runs as one kernel at decode from this many sorted rows (the header's EXL3C4_GD_FUSE_MIN_T; a build
+ * may move it to compare the two forms) */
+#ifndef GD_FUSE_ROWS
+#define GD_FUSE_ROWS EXL3C4_GD_FUSE_MIN_T
+#endif
+
 typedef struct Carve {
     int     pf;                                   /* the prefill path */
-    int64_t row_info, plan, xr, part, h, dacc, total;
+    int     gd1;                                  /* gate_up_down as one kernel (decode path, T >= GD_FUSE_MIN_T) */
+    int64_t row_info, plan, xr, part, h, dacc, sync, total;
     int64_t T, part_pitch, dacc_pitch, xr_pitch, h_pitch, max_chunks;
     int     split_gu, gu_lds_pitch, dn_lds_pitch;
 } Carve;
 
 /* The scratch of one launch with T sorted rows, each region 256-B aligned.
- *   decode path:  [row_info | gate_up split-K partial sums | down accumulations]
+ *   decode path:  [row_info | gate_up split-K partial sums | h (gate_up_down as one kernel) | down accumulations |
+ *                  sync (gate_up_down as one kernel)]
  *   prefill path: [row_info | plan | rotated input | gate_up sums | h (gate_up_down) | down accumulations]
  * row_info: each row's owner (and, decode path, chunk rows), written by the first kernel for those after it. */
 static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
@@ -118,8 +126,9 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
         k->part_pitch = rc;
         off += ALIGN_UP(s * T * rc * 4, 256);
     }
+    k->gd1 = op == EXL3C4_GU_DN && !k->pf && T >= GD_FUSE_ROWS;
     k->h = off;
-    if (k->pf && op == EXL3C4_GU_DN) {
+    if ((k->pf || k->gd1) && op == EXL3C4_GU_DN) {
         k->h_pitch = rc / 2;
         off += ALIGN_UP(T * k->h_pitch * 2, 256);
     }
@@ -137,6 +146,8 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
         k->dn_lds_pitch = (int)(kmax + 8);     /* padded: the 16 staged rows start in different LDS banks */
         off += ALIGN_UP(T * nmax * 4, 256);
     }
+    k->sync = off;
+    if (k->gd1) off += (T + 1) * EXL3C4_SYNC_STRIDE * 4;   /* the status word, a counter a row (256 B each) */
     k->total = off;
 }
 
@@ -182,7 +193,7 @@ static int check(const Exl3c4Op* o) {
             if (d->svh_stride & 1) return EXL3C4_E_ALIGN;
         }
     }
-    /* down stages a chunk's 16 input rows in LDS: at most 1536 columns (57 KiB with its accumulations) */
+    /* down stages a chunk's 16 input rows in LDS: at most 1536 columns (49 KiB) */
     for (int c = 0; c < o->n_class; ++c) {
         const int64_t kdn = op == EXL3C4_DOWN ? o->cls[c].cols : op == EXL3C4_GU_DN ? o->cls[c].rows / 2 : 0;
         if (kdn > 1536) return EXL3C4_E_UNSUPPORTED;
@@ -345,11 +356,52 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     return exl3c4_dev_zero_dead(&d, stream, NULL, NULL);
 }
 
+/* gate_up_down at decode as one kernel: the row counters and status zeroed, then k_gd (gate_up units, then down
+ * units waiting on their row's counter). */
+static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t) {
+    int rc;
+    Exl3c4Launch g;
+    base_args(o, k, s, &g);
+    down_classes(o, &g);                          /* cls: down's; gcls: gate_up's */
+    g.h_from_gu = 1;
+    g.ksplit = k->split_gu;
+    g.ksplit_log2 = log2i(k->split_gu);
+    g.n_grp = (int32_t)(max_rows(o) / 128);
+    g.lds_pitch_gu = k->gu_lds_pitch;
+    g.lds_pitch = k->dn_lds_pitch;
+    g.nblk = (int32_t)(o->y_cols / 128);
+    g.dacc = (float*)(s + k->dacc);
+    g.dacc_pitch = k->dacc_pitch;
+    g.sync = (int32_t*)(s + k->sync);
+    g.hbuf = (uint16_t*)(s + k->h);
+    g.hbuf_pitch = k->h_pitch;
+    if ((rc = exl3c4_dev_fill(g.sync, (o->T + 1) * EXL3C4_SYNC_STRIDE, stream)) != 0) return rc;
+    return exl3c4_dev_gd(&g, stream, EV(EXL3C4_K_GATE_UP_DOWN));
+}
+
+/* The kernels a launch runs (for exl3c4_launch_timed). */
+static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
+    const int op = o->op;
+    if (op == EXL3C4_PREP_GU) return kernel == EXL3C4_K_PREP;
+    if (k->pf) {
+        if (kernel == EXL3C4_K_PREP) return 1;                   /* the plan */
+        if (kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_EPI_GU) return op != EXL3C4_DOWN;
+        return kernel == EXL3C4_K_DOWN && op != EXL3C4_GATE_UP;
+    }
+    if (k->gd1) return kernel == EXL3C4_K_GATE_UP_DOWN;
+    switch (op) {
+    case EXL3C4_GATE_UP: return kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_EPI_GU;
+    case EXL3C4_DOWN:    return kernel == EXL3C4_K_DOWN;
+    default:             return kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_DOWN;
+    }
+}
+
 /* The launches of each op on the stream -- no planning pass: every workgroup finds its rows' expert itself.
  *   prep_gu       the input rotation
  *   gate_up       its GEMM (input rotation staged inside), then its epilogue
  *   down          its GEMM, whose workgroups stage (and rotate) their rows and finish their output blocks
- *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums */
+ *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums; from
+ *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1) */
 static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
@@ -369,6 +421,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     }
 
     if (k.pf) return launch_prefill(o, &k, s, stream, t);
+    if (k.gd1) return launch_gd1(o, &k, s, stream, t);
 
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
@@ -412,7 +465,12 @@ int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void*
 
 int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop) {
-    if (kernel < EXL3C4_K_PREP || kernel > EXL3C4_K_DOWN || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
+    int rc;
+    if (!o || !ev_start || !ev_stop) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    Carve k;
+    carve(o, o->T, &k);
+    if (!runs_kernel(o, &k, kernel)) return EXL3C4_E_INVAL;
     const Timed t = { kernel, ev_start, ev_stop };
     return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }
@@ -436,6 +494,17 @@ int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, in
         *split_stride = k.T * k.part_pitch;
         *splits = k.split_gu;
     }
+    return EXL3C4_OK;
+}
+
+int exl3c4_scratch_status(const Exl3c4Op* o, int64_t* offset) {
+    int rc;
+    if (!o || !offset) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    Carve k;
+    carve(o, o->T, &k);
+    if (!k.gd1) return EXL3C4_E_INVAL;
+    *offset = k.sync;
     return EXL3C4_OK;
 }
 

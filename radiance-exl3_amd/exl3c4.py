@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libexl3c4.so")
 
 DOWN, GATE_UP, PREP_GU, GU_DN = 0, 1, 2, 3
-K_PREP, K_GATE_UP, K_EPI_GU, K_DOWN = 0, 1, 2, 3
+K_PREP, K_GATE_UP, K_EPI_GU, K_DOWN, K_GATE_UP_DOWN = 0, 1, 2, 3, 4
+GD_FUSE_MIN_T = 32                  # gate_up_down runs as one kernel at decode from this many sorted rows
 CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 F16, BF16 = 0, 1
 STATUS = {0: "OK", -1: "RAD_E_SHAPE", -2: "RAD_E_DTYPE", -3: "RAD_E_ALIGN", -4: "RAD_E_STRIDE", -9: "RAD_E_SCHEMA",
@@ -67,6 +68,8 @@ def lib():
         L.exl3c4_scratch_partials.restype = C.c_int
         L.exl3c4_scratch_partials.argtypes = [C.POINTER(Op), _i32, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64),
                                               C.POINTER(_i32)]
+        L.exl3c4_scratch_status.restype = C.c_int
+        L.exl3c4_scratch_status.argtypes = [C.POINTER(Op), C.POINTER(_i64)]
         L.exl3c4_build_target.restype = C.c_char_p
         L.exl3c4_abi_version.restype = C.c_int
         _lib = L
@@ -228,6 +231,15 @@ def partial_sums(o: Op, scratch, gemm: int = 0):
         with np.errstate(over="ignore", invalid="ignore"):
             acc = (acc + raw[s * ss.value: s * ss.value + T * pitch.value].reshape(T, pitch.value)).astype(np.float32)
     return acc
+
+
+def launch_status(o: Op, scratch) -> int:
+    """The status word gate_up_down's single kernel left in `scratch` (0: good; 1: a wait gave up, the output is
+    void), or None when the launch of `o` does not run that kernel."""
+    off = _i64()
+    if lib().exl3c4_scratch_status(C.byref(o), C.byref(off)):
+        return None
+    return int(scratch[off.value: off.value + 4].cpu().numpy().view(np.int32)[0])
 
 
 def alloc_scratch(o: Op, device="cuda"):

@@ -235,6 +235,8 @@ class Dev:
         assert rc == expect, f"launch status {self.ex.STATUS.get(rc, rc)}"
         self.torch.cuda.synchronize()
         self.last = (o, s)
+        self.status = self.ex.launch_status(o, s) if rc == 0 else None
+        assert self.status in (None, 0), f"gate_up_down's single kernel left status {self.status}"
 
     def last_acc(self, gemm=0):
         """The f32 accumulations the last launch left in its scratch."""
@@ -274,6 +276,7 @@ class Dev:
         return y.cpu().numpy().view(np.uint16)
 
     def gate_up_down(self):
+        """gate_up_down's output; self.status is then None (two kernels) or 0 (one kernel, which went well)."""
         c = self.case
         N = max(d["rows"] for d in self.tabs["dn"])
         y = self.out(N)

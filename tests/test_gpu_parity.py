@@ -154,6 +154,44 @@ def test_ops_four_classes(torch_cuda):
     _check_all(case, "four-class")
 
 
+# ------------------------------------------------------------------------------------------ gate_up_down as one kernel
+# (decode path from 32 sorted rows: gate_up units and down units in one dispatch, each down unit waiting on its row's
+# counter; _check_all holds it to the bits of the gate_up -> down pair, which runs as two kernels)
+FUSED = {
+    "one-class": dict(seed=50, n_tok=8, top_k=6, n_expert=24, geoms=[(256, 128)], bits=4, cb="mul1", drop=0.1,
+                      protect_tail=2),
+    "two-class": dict(seed=51, n_tok=10, top_k=4, n_expert=12, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
+                      drop=0.2),
+    "four-class-mcg": dict(seed=52, n_tok=8, top_k=8, n_expert=16,
+                           geoms=[(256, 128), (256, 256), (128, 128), (256, 128)], bits=5, cb="mcg"),
+    "chunks-of-many-rows": dict(seed=53, n_tok=20, top_k=2, n_expert=3, geoms=[(256, 128)], bits=3, cb="3inst",
+                                x_bf16=True),
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED))
+def test_gate_up_down_as_one_kernel(torch_cuda, name):
+    import exl3c4
+    case = Case(**FUSED[name])
+    assert case.T >= exl3c4.GD_FUSE_MIN_T and (case.T < 64 or case.T < 8 * case.n_expert)
+    dev = _check_all(case, f"one kernel {name}")
+    assert dev.status == 0                             # the last launch (gate_up_down) ran as one kernel
+
+
+def test_gate_up_down_as_one_kernel_at_the_layer_geometry(torch_cuda):
+    """The decode layer's expert shapes (gate/up 2048 -> 512, down 512 -> 2048, K=4), 8 tokens top-10 over 128 experts:
+    the single kernel's bits equal the pair's, and replays agree."""
+    case = Case(seed=54, n_tok=8, top_k=10, n_expert=128, geoms=[(2048, 512)], bits=4, cb="mul1")
+    dev = Dev(case)
+    _say("one kernel, layer geometry")
+    gd = dev.gate_up_down()
+    assert dev.status == 0
+    y = dev.down(dev.gate_up(h_rot=1), h_rot=1)
+    assert np.array_equal(gd, y)
+    for _ in range(3):
+        assert np.array_equal(dev.gate_up_down(), gd)
+
+
 # ------------------------------------------------------------------------------------------ the prefill path
 # (T >= 8 n_expert rows: chunks of up to 64 rows, a plan, the rotation into scratch, the prefill GEMMs)
 def test_prefill_path_two_classes_several_chunks_with_drops(torch_cuda):
