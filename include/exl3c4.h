@@ -58,7 +58,7 @@ enum { EXL3C4_DOWN = 0, EXL3C4_GATE_UP = 1, EXL3C4_PREP_GU = 2, EXL3C4_GU_DN = 3
 /* Codebooks, numbered as common/exl3_decode.h:60 numbers them. */
 enum { EXL3C4_CB_3INST = 0, EXL3C4_CB_MCG = 1, EXL3C4_CB_MUL1 = 2 };
 /* Activation dtypes. */
-enum { EXL3C4_F16 = 0, EXL3C4_BF16 = 1 };
+enum { EXL3C4_F16 = 0, EXL3C4_BF16 = 1, EXL3C4_F32 = 2 };
 
 /* One class of experts (include/exl3_abi.h:186-206, 298-304): a weight table per plane. A table is a device pointer
  * array (its *_stride 0: entry j at ((void**)base)[j], the engine's form) or one stacked device buffer (entry j at base
@@ -146,6 +146,36 @@ int exl3c4_scratch_status(const Exl3c4Op* op, int64_t* offset);
  * include/exl3_encoding.h:45-48). */
 int exl3c4_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
                    int64_t w_pitch, void* stream);
+
+/* ------------------------------------------------------------------ the routing around the ops (device)
+ * What the radiance engine runs in front of and behind the routed-expert ops (router_topk, moe_scatter, moe_gather;
+ * the contract at include/exl3_abi.h:90-158), so that a whole MoE layer runs on this library. No counterpart in the
+ * reference device library, which leaves them to the engine; the semantics are the contract's and
+ * tests/ref/exl3_numpy.py:223-242's (the scatter). Each returns before writing anything when it refuses. */
+
+/* The router: for each of n_tok tokens, the softmax over all n_expert logits (row t at logits + t * pitch elements,
+ * dtype EXL3C4_F32 / F16 / BF16), its top_k experts by probability -- ties to the lower id; the softmax is monotone in
+ * the logit, so they are ranked by logit -- and their probabilities, renormalised to sum to one when renorm is 1:
+ * expert_ids i32 [n_tok][top_k] (descending probability), expert_w f32 [n_tok][top_k]. f32 arithmetic: m = max logit,
+ * p_e = expf(l_e - m) / sum over all e. 1 <= top_k <= min(n_expert, 64), n_expert <= 65536. */
+int exl3c4_router_topk(const void* logits, int32_t logits_dtype, int64_t n_tok, int64_t n_expert, int64_t pitch,
+                       int32_t top_k, int32_t renorm, int32_t* expert_ids, float* expert_w, void* stream);
+
+/* moe_scatter: the flat pairs p = t * top_k + slot (T = n_tok * top_k of them) grouped by expert by a STABLE counting
+ * sort (include/exl3_abi.h:109-123): expert_offset i32 [n_expert + 1] (expert e's rows [off[e], off[e+1]), off[n_expert]
+ * the live count), sorted_tok i32 [T] (-1 past the live count), and, when not null, expert_count i32 [n_expert] and
+ * row_of i32 [T] (the sorted row of pair p, -1 for a dropped pair: what the gather reads). A pair whose expert is
+ * outside [expert_base, expert_base + n_expert) is dropped. One workgroup; n_expert <= 2048. */
+int exl3c4_moe_scatter(const int32_t* expert_ids, int64_t n_tok, int32_t top_k, int64_t expert_base,
+                       int64_t n_expert, int32_t* sorted_tok, int32_t* expert_offset, int32_t* expert_count,
+                       int32_t* row_of, void* stream);
+
+/* moe_gather: out[t][c] = f16( sum over slots s = 0 .. top_k-1 in ascending order, of the pairs with a row, of
+ * expert_w[t][s] * y[row_of[t * top_k + s]][c] ), accumulated in f32 as one product and one add a slot (the north
+ * star's layer output: the weighted sum in fp32, cast to fp16, round to nearest even). y: the down op's output rows,
+ * dtype EXL3C4_BF16 or F16, y_pitch elements apart; out f16, out_pitch apart. cols % 8 == 0. */
+int exl3c4_moe_gather(const void* y, int32_t y_dtype, int64_t y_pitch, const float* expert_w, const int32_t* row_of,
+                      int64_t n_tok, int32_t top_k, int64_t cols, void* out, int64_t out_pitch, void* stream);
 
 /* ------------------------------------------------------------------ the stored form (host, load time) */
 /* Bytes of the stored record of a [rows, cols] weight at K bits: rows * cols * K / 8. */

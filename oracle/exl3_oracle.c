@@ -494,8 +494,8 @@ int or_gate_up_down(const OrOp* gu, const OrOp* dn) {
 
 /* include/exl3_abi.h:109-123; tests/ref/exl3_numpy.py:223-242: count per expert, exclusive prefix, then place
  * each flat index in ascending order (stable); a slot outside the owned range is not placed. */
-void or_moe_scatter(const int32_t* ids, int64_t n_tok, int64_t top_k, int64_t base, int64_t n_expert,
-                    int32_t* sorted_tok, int32_t* off) {
+void or_moe_scatter_full(const int32_t* ids, int64_t n_tok, int64_t top_k, int64_t base, int64_t n_expert,
+                         int32_t* sorted_tok, int32_t* off, int32_t* count, int32_t* row_of) {
     const int64_t n = n_tok * top_k;
     int64_t* fill = (int64_t*)calloc((size_t)n_expert + 1, sizeof(int64_t));
     for (int64_t e = 0; e <= n_expert; ++e) off[e] = 0;
@@ -503,11 +503,82 @@ void or_moe_scatter(const int32_t* ids, int64_t n_tok, int64_t top_k, int64_t ba
         const int64_t e = (int64_t)ids[i] - base;
         if (e >= 0 && e < n_expert) off[e + 1]++;
     }
+    if (count)
+        for (int64_t e = 0; e < n_expert; ++e) count[e] = off[e + 1];
     for (int64_t e = 0; e < n_expert; ++e) off[e + 1] += off[e];
     for (int64_t i = 0; i < n; ++i) sorted_tok[i] = -1;
     for (int64_t i = 0; i < n; ++i) {
         const int64_t e = (int64_t)ids[i] - base;
-        if (e >= 0 && e < n_expert) sorted_tok[off[e] + fill[e]++] = (int32_t)i;
+        int32_t pos = -1;
+        if (e >= 0 && e < n_expert) {
+            pos = (int32_t)(off[e] + fill[e]++);
+            sorted_tok[pos] = (int32_t)i;
+        }
+        if (row_of) row_of[i] = pos;
     }
     free(fill);
+}
+
+void or_moe_scatter(const int32_t* ids, int64_t n_tok, int64_t top_k, int64_t base, int64_t n_expert,
+                    int32_t* sorted_tok, int32_t* off) {
+    or_moe_scatter_full(ids, n_tok, top_k, base, n_expert, sorted_tok, off, NULL, NULL);
+}
+
+/* a ranks before b: the larger logit, or the same logit and the lower id; a NaN logit after every number */
+static int rank_before(float la, int64_t ea, float lb, int64_t eb) {
+    const int na = la != la, nb = lb != lb;
+    if (na != nb) return nb;
+    if (!na && la != lb) return la > lb;
+    return ea < eb;
+}
+
+void or_router_topk(const float* logits, int64_t n_tok, int64_t n_expert, int64_t pitch, int top_k, int renorm,
+                    int32_t* ids, float* w) {
+    for (int64_t t = 0; t < n_tok; ++t) {
+        const float* l = logits + t * pitch;
+        double m = -INFINITY, s = 0.0, sk = 0.0, p[64];
+        for (int64_t e = 0; e < n_expert; ++e)
+            if (l[e] > m) m = l[e];
+        for (int64_t e = 0; e < n_expert; ++e) s += exp((double)l[e] - m);
+        float prev_l = 0.f;
+        int64_t prev_e = -1;
+        for (int j = 0; j < top_k; ++j) {
+            int64_t be = -1;
+            for (int64_t e = 0; e < n_expert; ++e) {
+                if (j > 0 && !rank_before(prev_l, prev_e, l[e], e)) continue;
+                if (be < 0 || rank_before(l[e], e, l[be], be)) be = e;
+            }
+            prev_l = l[be];
+            prev_e = be;
+            ids[t * top_k + j] = (int32_t)be;
+            p[j] = exp((double)l[be] - m) / s;
+            sk += p[j];
+        }
+        for (int j = 0; j < top_k; ++j) w[t * top_k + j] = (float)(renorm ? p[j] / sk : p[j]);
+    }
+}
+
+static float or_bits_to_f32(uint16_t b, int bf16) {
+    if (bf16) {
+        const uint32_t u = (uint32_t)b << 16;
+        float f;
+        memcpy(&f, &u, 4);
+        return f;
+    }
+    return or_half_to_float(b);
+}
+
+void or_moe_gather(const uint16_t* y, int y_bf16, int64_t y_pitch, const float* w, const int32_t* row_of,
+                   int64_t n_tok, int top_k, int64_t cols, uint16_t* out, int64_t out_pitch) {
+    for (int64_t t = 0; t < n_tok; ++t)
+        for (int64_t c = 0; c < cols; ++c) {
+            float acc = 0.f;
+            for (int s = 0; s < top_k; ++s) {
+                const int32_t r = row_of[t * top_k + s];
+                if (r < 0) continue;
+                const float prod = w[t * top_k + s] * or_bits_to_f32(y[(int64_t)r * y_pitch + c], y_bf16);
+                acc = acc + prod;
+            }
+            out[t * out_pitch + c] = or_f32_to_f16(acc);
+        }
 }

@@ -117,6 +117,24 @@ int or_gate_up_down(const OrOp* gu, const OrOp* dn);
  * are dropped. sorted_tok[n_tok*top_k] (-1 past the live count), expert_offset[n_expert + 1]. */
 void or_moe_scatter(const int32_t* expert_ids, int64_t n_tok, int64_t top_k, int64_t expert_base,
                     int64_t n_expert, int32_t* sorted_tok, int32_t* expert_offset);
+/* The same, with expert_count[n_expert] (rows per expert) and row_of[n_tok*top_k] (the sorted row of each flat pair,
+ * -1 for a dropped pair); either may be null. */
+void or_moe_scatter_full(const int32_t* expert_ids, int64_t n_tok, int64_t top_k, int64_t expert_base,
+                         int64_t n_expert, int32_t* sorted_tok, int32_t* expert_offset, int32_t* expert_count,
+                         int32_t* row_of);
+
+/* router_topk (include/exl3_abi.h:96-98: softmax over ALL logits, top_k, optional renormalisation), in double: the
+ * top_k ids ranked by probability with ties to the lower id (the softmax is monotone in the logit, so by logit; a NaN
+ * logit ranks last), p_e = exp(l_e - m) / sum over all e of exp(l - m), renormalised over the top_k when asked;
+ * expert_w as f32 of the double. */
+void or_router_topk(const float* logits, int64_t n_tok, int64_t n_expert, int64_t pitch, int top_k, int renorm,
+                    int32_t* expert_ids, float* expert_w);
+
+/* moe_gather (include/exl3_abi.h:104-108, the north star's layer output): out[t][c] = f16 RNE of the f32 sum, over the
+ * slots in ascending order with a row, of the f32 product expert_w[t][s] * y[row][c] (one rounding each). y bf16 or
+ * f16 bits. */
+void or_moe_gather(const uint16_t* y, int y_bf16, int64_t y_pitch, const float* expert_w, const int32_t* row_of,
+                   int64_t n_tok, int top_k, int64_t cols, uint16_t* out, int64_t out_pitch);
 
 #ifdef __cplusplus
 }

@@ -83,6 +83,9 @@ def _declare(L):
     L.or_gate_up_down.restype = C.c_int
     L.or_gate_up_down.argtypes = [_p, _p]
     L.or_moe_scatter.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p]
+    L.or_moe_scatter_full.argtypes = [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]
+    L.or_router_topk.argtypes = [_p, _i64, _i64, _i64, C.c_int, C.c_int, _p, _p]
+    L.or_moe_gather.argtypes = [_p, C.c_int, _i64, _p, _p, _i64, C.c_int, _i64, _p, _i64]
     L.or_prologue.restype = C.c_int
     L.or_prologue.argtypes = [_p, _p, _i64, _p]
 
@@ -232,6 +235,40 @@ def moe_scatter(expert_ids: np.ndarray, n_expert: int, expert_base: int = 0):
     off = np.zeros(n_expert + 1, np.int32)
     lib().or_moe_scatter(_ptr(ids), n_tok, top_k, expert_base, n_expert, _ptr(st), _ptr(off))
     return st, off
+
+
+def moe_scatter_full(expert_ids: np.ndarray, n_expert: int, expert_base: int = 0):
+    """or_moe_scatter_full: (sorted_tok, expert_offset, expert_count, row_of)."""
+    ids = np.ascontiguousarray(expert_ids, dtype=np.int32)
+    n_tok, top_k = ids.shape
+    st = np.zeros(n_tok * top_k, np.int32)
+    off = np.zeros(n_expert + 1, np.int32)
+    cnt = np.zeros(n_expert, np.int32)
+    row_of = np.zeros(n_tok * top_k, np.int32)
+    lib().or_moe_scatter_full(_ptr(ids), n_tok, top_k, expert_base, n_expert, _ptr(st), _ptr(off), _ptr(cnt),
+                              _ptr(row_of))
+    return st, off, cnt, row_of
+
+
+def router_topk(logits: np.ndarray, top_k: int, renorm: bool = True):
+    """or_router_topk on f32 logits [n_tok, n_expert]: (ids i32 [n_tok, top_k], w f32 [n_tok, top_k])."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    n_tok, n_expert = lg.shape
+    ids = np.zeros((n_tok, top_k), np.int32)
+    w = np.zeros((n_tok, top_k), np.float32)
+    lib().or_router_topk(_ptr(lg), n_tok, n_expert, n_expert, top_k, int(renorm), _ptr(ids), _ptr(w))
+    return ids, w
+
+
+def moe_gather(y_bits: np.ndarray, y_bf16: bool, expert_w: np.ndarray, row_of: np.ndarray, n_tok: int, top_k: int):
+    """or_moe_gather: f16 bits [n_tok, cols] from y bits [T, cols] (bf16 or f16)."""
+    y = np.ascontiguousarray(y_bits).view(np.uint16)
+    w = np.ascontiguousarray(expert_w, dtype=np.float32)
+    ro = np.ascontiguousarray(row_of, dtype=np.int32)
+    cols = y.shape[1]
+    out = np.zeros((n_tok, cols), np.uint16)
+    lib().or_moe_gather(_ptr(y), int(y_bf16), cols, _ptr(w), _ptr(ro), n_tok, top_k, cols, _ptr(out), cols)
+    return out
 
 
 # ------------------------------------------------------------------------------------------ the ops

@@ -72,6 +72,13 @@ int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
+/* the routing (exl3c4_route.hip) */
+int exl3c4_dev_router(const void* logits, int32_t dtype, int64_t n_tok, int32_t n_expert, int64_t pitch, int32_t top_k,
+                      int32_t renorm, int32_t* ids, float* w, void* stream);
+int exl3c4_dev_scatter(const int32_t* ids, int64_t T, int64_t base, int32_t n_expert, int32_t* sorted, int32_t* off,
+                       int32_t* count, int32_t* row_of, void* stream);
+int exl3c4_dev_gather(const void* y, int32_t y_dtype, int64_t y_pitch, const float* w, const int32_t* row_of,
+                      int64_t n_tok, int32_t top_k, int64_t cols, void* out, int64_t out_pitch, void* stream);
 int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,
                        int64_t w_pitch, void* stream);
 

@@ -68,6 +68,12 @@ def lib():
         L.exl3c4_scratch_partials.restype = C.c_int
         L.exl3c4_scratch_partials.argtypes = [C.POINTER(Op), _i32, C.POINTER(_i64), C.POINTER(_i64), C.POINTER(_i64),
                                               C.POINTER(_i32)]
+        L.exl3c4_router_topk.restype = C.c_int
+        L.exl3c4_router_topk.argtypes = [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _p, _p]
+        L.exl3c4_moe_scatter.restype = C.c_int
+        L.exl3c4_moe_scatter.argtypes = [_p, _i64, _i32, _i64, _i64, _p, _p, _p, _p, _p]
+        L.exl3c4_moe_gather.restype = C.c_int
+        L.exl3c4_moe_gather.argtypes = [_p, _i32, _i64, _p, _p, _i64, _i32, _i64, _p, _i64, _p]
         L.exl3c4_scratch_status.restype = C.c_int
         L.exl3c4_scratch_status.argtypes = [C.POINTER(Op), C.POINTER(_i64)]
         L.exl3c4_build_target.restype = C.c_char_p
@@ -240,6 +246,39 @@ def launch_status(o: Op, scratch) -> int:
     if lib().exl3c4_scratch_status(C.byref(o), C.byref(off)):
         return None
     return int(scratch[off.value: off.value + 4].cpu().numpy().view(np.int32)[0])
+
+
+# ------------------------------------------------------------------------------------------ the routing (device)
+F32 = 2
+
+
+def _dt(t):
+    import torch
+    return {torch.float32: F32, torch.float16: 0, torch.bfloat16: 1}[t.dtype]
+
+
+def router_topk(logits, top_k: int, renorm: bool = True, ids=None, w=None, stream=None) -> int:
+    """exl3c4_router_topk on a device tensor [n_tok, n_expert] (f32 / f16 / bf16): fills ids (i32) and w (f32)
+    [n_tok, top_k]; returns the status."""
+    n_tok, n_expert = logits.shape
+    return int(lib().exl3c4_router_topk(_ptr(logits), _dt(logits), n_tok, n_expert, logits.stride(0), top_k,
+                                        int(renorm), _ptr(ids), _ptr(w), _stream(stream)))
+
+
+def moe_scatter(ids, n_expert: int, sorted_tok, expert_offset, expert_count=None, row_of=None, expert_base: int = 0,
+                stream=None) -> int:
+    """exl3c4_moe_scatter on device i32 tensors: ids [n_tok, top_k] in; the rest out."""
+    n_tok, top_k = ids.shape
+    return int(lib().exl3c4_moe_scatter(_ptr(ids), n_tok, top_k, expert_base, n_expert, _ptr(sorted_tok),
+                                        _ptr(expert_offset), _ptr(expert_count), _ptr(row_of), _stream(stream)))
+
+
+def moe_gather(y, y_bf16: bool, w, row_of, out, stream=None) -> int:
+    """exl3c4_moe_gather: y int16 bits [T, cols] (bf16 or f16), w f32 [n_tok, top_k], row_of i32, out int16 bits
+    [n_tok, cols] (f16)."""
+    n_tok, top_k = w.shape
+    return int(lib().exl3c4_moe_gather(_ptr(y), 1 if y_bf16 else 0, y.stride(0), _ptr(w), _ptr(row_of), n_tok, top_k,
+                                       y.shape[1], _ptr(out), out.stride(0), _stream(stream)))
 
 
 def alloc_scratch(o: Op, device="cuda"):

@@ -26,7 +26,7 @@ class Case:
     """n_expert experts of n_class classes: gate_up [2W_c, H_c] and down [H_c, W_c] per expert, class c = e % n_class."""
 
     def __init__(self, seed, n_tok, top_k, n_expert, geoms, bits, cb, drop=0.0, protect_tail=0, x_bf16=False,
-                 routing="uniform"):
+                 routing="uniform", expert_ids=None):
         rng = np.random.default_rng(seed)
         self.rng = rng
         self.n_tok, self.top_k, self.n_expert, self.bits, self.cb = n_tok, top_k, n_expert, bits, cb
@@ -47,7 +47,9 @@ class Case:
             self.x = (x.view(np.uint32) >> 16).astype(np.uint16)          # bf16 bits (truncation: any bits are fine)
         else:
             self.x = x.astype(np.float16).view(np.uint16)
-        if routing == "zipf":
+        if expert_ids is not None:                          # a given routing (the device router's, say)
+            ids, w = np.asarray(expert_ids, np.int32), None
+        elif routing == "zipf":
             ids, w = syn.zipf_topk(rng, n_tok, n_expert, top_k)
         else:
             ids, w = syn.router_topk(rng.standard_normal((n_tok, n_expert)), top_k)
