@@ -157,7 +157,7 @@ int exl3c4_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits,
  * dtype EXL3C4_F32 / F16 / BF16), its top_k experts by probability -- ties to the lower id; the softmax is monotone in
  * the logit, so they are ranked by logit -- and their probabilities, renormalised to sum to one when renorm is 1:
  * expert_ids i32 [n_tok][top_k] (descending probability), expert_w f32 [n_tok][top_k]. f32 arithmetic: m = max logit,
- * p_e = expf(l_e - m) / sum over all e. 1 <= top_k <= min(n_expert, 64), n_expert <= 65536. */
+ * p_e = expf(l_e - m) / sum over all e. 1 <= top_k <= min(n_expert, 64), n_expert <= 1024. */
 int exl3c4_router_topk(const void* logits, int32_t logits_dtype, int64_t n_tok, int64_t n_expert, int64_t pitch,
                        int32_t top_k, int32_t renorm, int32_t* expert_ids, float* expert_w, void* stream);
 
@@ -169,6 +169,13 @@ int exl3c4_router_topk(const void* logits, int32_t logits_dtype, int64_t n_tok, 
 int exl3c4_moe_scatter(const int32_t* expert_ids, int64_t n_tok, int32_t top_k, int64_t expert_base,
                        int64_t n_expert, int32_t* sorted_tok, int32_t* expert_offset, int32_t* expert_count,
                        int32_t* row_of, void* stream);
+
+/* router_topk_scatter: the two above on the same logits (the fused form the contract names, include/exl3_abi.h:96-98),
+ * with expert_base 0; up to 16 tokens in one workgroup (one launch), more as the two launches. */
+int exl3c4_router_topk_scatter(const void* logits, int32_t logits_dtype, int64_t n_tok, int64_t n_expert,
+                               int64_t pitch, int32_t top_k, int32_t renorm, int32_t* expert_ids, float* expert_w,
+                               int32_t* sorted_tok, int32_t* expert_offset, int32_t* expert_count, int32_t* row_of,
+                               void* stream);
 
 /* moe_gather: out[t][c] = f16( sum over slots s = 0 .. top_k-1 in ascending order, of the pairs with a row, of
  * expert_w[t][s] * y[row_of[t * top_k + s]][c] ), accumulated in f32 as one product and one add a slot (the north

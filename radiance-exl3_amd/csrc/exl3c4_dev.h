@@ -77,6 +77,9 @@ int exl3c4_dev_router(const void* logits, int32_t dtype, int64_t n_tok, int32_t 
                       int32_t renorm, int32_t* ids, float* w, void* stream);
 int exl3c4_dev_scatter(const int32_t* ids, int64_t T, int64_t base, int32_t n_expert, int32_t* sorted, int32_t* off,
                        int32_t* count, int32_t* row_of, void* stream);
+int exl3c4_dev_route_scatter(const void* logits, int32_t dtype, int32_t n_tok, int32_t n_expert, int64_t pitch,
+                             int32_t top_k, int32_t renorm, int32_t* ids, float* w, int32_t* sorted, int32_t* off,
+                             int32_t* count, int32_t* row_of, void* stream);
 int exl3c4_dev_gather(const void* y, int32_t y_dtype, int64_t y_pitch, const float* w, const int32_t* row_of,
                       int64_t n_tok, int32_t top_k, int64_t cols, void* out, int64_t out_pitch, void* stream);
 int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook, void* w_hat,

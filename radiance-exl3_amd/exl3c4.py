@@ -72,6 +72,8 @@ def lib():
         L.exl3c4_router_topk.argtypes = [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _p, _p]
         L.exl3c4_moe_scatter.restype = C.c_int
         L.exl3c4_moe_scatter.argtypes = [_p, _i64, _i32, _i64, _i64, _p, _p, _p, _p, _p]
+        L.exl3c4_router_topk_scatter.restype = C.c_int
+        L.exl3c4_router_topk_scatter.argtypes = [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]
         L.exl3c4_moe_gather.restype = C.c_int
         L.exl3c4_moe_gather.argtypes = [_p, _i32, _i64, _p, _p, _i64, _i32, _i64, _p, _i64, _p]
         L.exl3c4_scratch_status.restype = C.c_int
@@ -271,6 +273,16 @@ def moe_scatter(ids, n_expert: int, sorted_tok, expert_offset, expert_count=None
     n_tok, top_k = ids.shape
     return int(lib().exl3c4_moe_scatter(_ptr(ids), n_tok, top_k, expert_base, n_expert, _ptr(sorted_tok),
                                         _ptr(expert_offset), _ptr(expert_count), _ptr(row_of), _stream(stream)))
+
+
+def router_topk_scatter(logits, top_k: int, renorm: bool, ids, w, sorted_tok, expert_offset, expert_count=None,
+                        row_of=None, stream=None) -> int:
+    """exl3c4_router_topk_scatter: the router and the scatter in one call (one launch up to 16 tokens)."""
+    n_tok, n_expert = logits.shape
+    return int(lib().exl3c4_router_topk_scatter(_ptr(logits), _dt(logits), n_tok, n_expert, logits.stride(0), top_k,
+                                                int(renorm), _ptr(ids), _ptr(w), _ptr(sorted_tok),
+                                                _ptr(expert_offset), _ptr(expert_count), _ptr(row_of),
+                                                _stream(stream)))
 
 
 def moe_gather(y, y_bf16: bool, w, row_of, out, stream=None) -> int:

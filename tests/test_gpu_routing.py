@@ -95,6 +95,34 @@ def test_scatter_matches_the_oracle(torch_cuda, n_tok, top_k, n_expert, base, ki
         assert np.array_equal(g, w_), name
 
 
+@pytest.mark.parametrize("n_tok", [8, 16, 40])
+def test_router_topk_scatter_matches_the_oracle(torch_cuda, n_tok):
+    """The fused entry (one workgroup up to 16 tokens, the two launches beyond) against the oracle's router then
+    scatter."""
+    import exl3c4
+    import oracle
+    torch = torch_cuda
+    E, top_k = 512, 10
+    print(f"router_topk_scatter {n_tok} tokens", flush=True)
+    rng = np.random.default_rng(100 + n_tok)
+    lg = rng.standard_normal((n_tok, E)).astype(np.float32)
+    lg[1] = np.round(lg[1] * 2) / 2                              # ties
+    T = n_tok * top_k
+    ids = torch.full((n_tok, top_k), -7, dtype=torch.int32, device="cuda")
+    w = torch.full((n_tok, top_k), -7.0, dtype=torch.float32, device="cuda")
+    st = torch.full((T,), -7, dtype=torch.int32, device="cuda")
+    off = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda")
+    cnt = torch.full((E,), -7, dtype=torch.int32, device="cuda")
+    row_of = torch.full((T,), -7, dtype=torch.int32, device="cuda")
+    assert exl3c4.router_topk_scatter(torch.from_numpy(lg).cuda(), top_k, True, ids, w, st, off, cnt, row_of) == 0
+    torch.cuda.synchronize()
+    ids_o, w_o = oracle.router_topk(lg, top_k, True)
+    assert np.array_equal(ids.cpu().numpy(), ids_o) and np.allclose(w.cpu().numpy(), w_o, rtol=2e-6, atol=0)
+    want = oracle.moe_scatter_full(ids_o, E)
+    for g, w_, name in zip((st, off, cnt, row_of), want, ("sorted_tok", "expert_offset", "expert_count", "row_of")):
+        assert np.array_equal(g.cpu().numpy(), w_), name
+
+
 @pytest.mark.parametrize("y_bf16", [True, False])
 def test_gather_is_bit_exact(torch_cuda, y_bf16):
     import exl3c4

@@ -135,6 +135,8 @@ def test_routing_refusals_are_decided_on_the_host():
     assert L.exl3c4_router_topk(C.c_void_p(0x10002), exl3c4.F32, 8, 512, 512, 10, 1, p, p, None) == -3
     assert L.exl3c4_router_topk(p, exl3c4.F32, 8, 512, 512, 10, 2, p, p, None) == -12
     assert L.exl3c4_router_topk(None, exl3c4.F32, 8, 512, 512, 10, 1, p, p, None) == -12
+    assert L.exl3c4_router_topk(p, exl3c4.F32, 8, 2048, 2048, 10, 1, p, p, None) == -18   # logits held in registers
+    assert L.exl3c4_router_topk_scatter(p, exl3c4.F32, 8, 512, 512, 10, 1, p, p, p, None, None, None, None) == -12
     # scatter: expert count the one-workgroup sort holds
     assert L.exl3c4_moe_scatter(p, 8, 10, 0, 4096, p, p, None, None, None) == -18
     assert L.exl3c4_moe_scatter(p, 8, 0, 0, 512, p, p, None, None, None) == -1
