@@ -70,14 +70,16 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // The normalised Sylvester Hadamard over one 128-block held by a wave, lane l holding x[l] (v0) and x[l + 64] (v1):
 // the butterfly stages h = 1 .. 64 in the reference's order, each (a + b) low and (a - b) high in f32, then one f32
 // multiply by 1/sqrt(128) (common/exl3_decode.c:172-189) -- the same roundings, so the same bits.
-// The partners are moved without LDS: DPP for h = 1, 2 (quad_perm), 4 (row_ror 4 or 12), 8 (row_ror 8); gfx950's
-// permlane swaps for 16 and 32, which leave each lane the pair's low-half value and its high-half value.
-template <int CTRL> __device__ __forceinline__ float dpp_f(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ void bfly(float& v, float p, bool hi) { v = hi ? p - v : v + p; }
-// h = 4: lane l's partner is l - 4 (row_ror 4) when bit 2 of l is set, else l + 4 (row_ror 12). Both moves sit in one
-// asm block so that neither can be sunk under a partial exec mask, where a DPP read of an inactive lane is void.
+// Each stage is one fused multiply-add by +-1 (exact product, one rounding: the same value as the add or the
+// subtract). For h = 1, 2, 8 it is one v_fmac_f32 whose partner operand comes by DPP (quad_perm, row_ror 8): v += c p
+// with c = -1 on the lanes whose bit h is set, which leaves those lanes the NEGATED result (v - p = -(p - v)); the
+// partner of a lane has the same lower bits, hence the same sign, so c needs no correction, and the signs are undone
+// by the final multiply (by -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of the lane are set). h = 4:
+// the partner is l - 4 (row_ror 4) when bit 2 of l is set, else l + 4 (row_ror 12); both moves sit in one asm block
+// so that neither can be sunk under a partial exec mask, where a DPP read of an inactive lane is void. h = 16, 32:
+// gfx950's permlane swaps leave each lane the pair's low-half value and its high-half value, v = lo + c up.
+#define HAD_DPP(v, c, CTRL) asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:0xf bank_mask:0xf" \
+                                         : "+v"(v) : "v"(c))
 __device__ __forceinline__ float partner4(float v, bool hi) {
     float a, b;
     asm volatile("s_nop 1\n\tv_mov_b32_dpp %0, %2 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
@@ -85,7 +87,7 @@ __device__ __forceinline__ float partner4(float v, bool hi) {
                  : "=&v"(a), "=&v"(b) : "v"(v));
     return hi ? a : b;
 }
-template <int H> __device__ __forceinline__ void bfly_swap(float& v, bool hi) {
+template <int H> __device__ __forceinline__ void bfly_swap(float& v, float c) {
     const unsigned u = __builtin_bit_cast(unsigned, v);
     unsigned lo_u, up_u;
     if constexpr (H == 16) {
@@ -95,31 +97,28 @@ template <int H> __device__ __forceinline__ void bfly_swap(float& v, bool hi) {
         const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
         lo_u = r[0]; up_u = r[1];
     }
-    const float lo = __builtin_bit_cast(float, lo_u), up = __builtin_bit_cast(float, up_u);
-    v = hi ? lo - up : lo + up;
+    v = fmaf(c, __builtin_bit_cast(float, up_u), __builtin_bit_cast(float, lo_u));
 }
 __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
-    bool hi = lane & 1;
-    bfly(v0, dpp_f<0xB1>(v0), hi);                 // quad_perm [1,0,3,2]
-    bfly(v1, dpp_f<0xB1>(v1), hi);
-    hi = lane & 2;
-    bfly(v0, dpp_f<0x4E>(v0), hi);                 // quad_perm [2,3,0,1]
-    bfly(v1, dpp_f<0x4E>(v1), hi);
-    hi = lane & 4;
-    bfly(v0, partner4(v0, hi), hi);
-    bfly(v1, partner4(v1, hi), hi);
-    hi = lane & 8;
-    bfly(v0, dpp_f<0x128>(v0), hi);
-    bfly(v1, dpp_f<0x128>(v1), hi);
-    hi = lane & 16;
-    bfly_swap<16>(v0, hi);
-    bfly_swap<16>(v1, hi);
-    hi = lane & 32;
-    bfly_swap<32>(v0, hi);
-    bfly_swap<32>(v1, hi);
+    const float c1 = (lane & 1) ? -1.f : 1.f, c2 = (lane & 2) ? -1.f : 1.f, c4 = (lane & 4) ? -1.f : 1.f;
+    const float c8 = (lane & 8) ? -1.f : 1.f, c16 = (lane & 16) ? -1.f : 1.f, c32 = (lane & 32) ? -1.f : 1.f;
+    HAD_DPP(v0, c1, "quad_perm:[1,0,3,2]");
+    HAD_DPP(v1, c1, "quad_perm:[1,0,3,2]");
+    HAD_DPP(v0, c2, "quad_perm:[2,3,0,1]");
+    HAD_DPP(v1, c2, "quad_perm:[2,3,0,1]");
+    const bool hi4 = lane & 4;
+    v0 = fmaf(partner4(v0, hi4), c4, v0);
+    v1 = fmaf(partner4(v1, hi4), c4, v1);
+    HAD_DPP(v0, c8, "row_ror:8");
+    HAD_DPP(v1, c8, "row_ror:8");
+    bfly_swap<16>(v0, c16);
+    bfly_swap<16>(v1, c16);
+    bfly_swap<32>(v0, c32);
+    bfly_swap<32>(v1, c32);
     const float a = v0 + v1, b = v0 - v1;
-    v0 = a * kHadScale;
-    v1 = b * kHadScale;
+    const float sc = (__builtin_popcount(lane & 15) & 1) ? -kHadScale : kHadScale;
+    v0 = a * sc;
+    v1 = b * sc;
 }
 
 // The expert owning sorted row i -- e with off[e] <= i < off[e + 1], or -1 (include/exl3_abi.h:136-141) -- found
@@ -418,22 +417,12 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
     }
 }
 
-// gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
-// sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
-// values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
-// 187-212).
-template <bool COH>
-__device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
-                                              int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
-    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
-    const int n0 = b * 128 + lane, n1 = n0 + 64;
-    const int width = K.rows / 2;
-    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
-    const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
-    const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
-    const int col[4] = { n0, n1, width + n0, width + n1 };
-    float acc[4];
-    sum_splits4<COH>(a, i, col, acc);
+// gate_up's epilogue on one 128-column block of a row, lane l holding gate columns l, l + 64 (acc[0], acc[1]) and up
+// columns l, l + 64 (acc[2], acc[3]) of the block's f32 sums, svh of those four columns and (h_rot) dn_suh of the two:
+// had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))).
+__device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0, uint16_t sg1, uint16_t su0,
+                                             uint16_t su1, uint16_t d0, uint16_t d1, int h_rot, int lane,
+                                             uint16_t& v0, uint16_t& v1) {
     float g0 = acc[0], g1 = acc[1], u0 = acc[2], u1 = acc[3];
     had128_wave(g0, g1, lane);
     had128_wave(u0, u1, lane);
@@ -451,6 +440,25 @@ __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c
     had128_wave(r0, r1, lane);
     v0 = f2h(r0);
     v1 = f2h(r1);
+}
+
+// gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
+// sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
+// values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
+// 187-212).
+template <bool COH>
+__device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
+                                              int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
+    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
+    const int n0 = b * 128 + lane, n1 = n0 + 64;
+    const int width = K.rows / 2;
+    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
+    const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
+    const int col[4] = { n0, n1, width + n0, width + n1 };
+    float acc[4];
+    sum_splits4<COH>(a, i, col, acc);
+    gate_up_math(acc, sg0, sg1, su0, su1, d0, d1, h_rot, lane, v0, v1);
 }
 
 typedef const uint32_t __attribute__((address_space(1)))* gu32p;
@@ -864,49 +872,166 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
     if (tid == 0) a.plan[0] = min(carry_s, a.max_chunks);
 }
 
-// The rotation into scratch, one wave per (sorted row, half, 128-block): gate_up's xr (halves 0 and 1: suh, suh1 of
-// the row's expert, token rows in) or down's rotated h (half 0: down's suh, sorted rows in). Rows no run holds are
-// not written (nothing reads them); a negative sorted_tok gives zeros.
+// had128 over 128-blocks held 8 consecutive elements a lane (lane l of a 16-lane row: elements 8 (l % 16) .. + 7 of
+// its block): the stages h = 1, 2, 4 inside the lane, h = 8, 16, 32, 64 across lanes l ^ 1, ^ 2, ^ 4, ^ 8 (within the
+// row) as in had128_wave -- v_fmac by +-1 with a DPP partner, negated results where the lane bit is set, undone by
+// the sign of the final scale. The same roundings as the reference's stages, so the same bits.
+__device__ __forceinline__ void had128_x8(float (&v)[8], int lane) {
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (!(j & h)) {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+    const float c1 = (lane & 1) ? -1.f : 1.f, c2 = (lane & 2) ? -1.f : 1.f, c4 = (lane & 4) ? -1.f : 1.f;
+    const float c8 = (lane & 8) ? -1.f : 1.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c1, "quad_perm:[1,0,3,2]");
+#pragma unroll
+    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c2, "quad_perm:[2,3,0,1]");
+    const bool hi4 = lane & 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = fmaf(partner4(v[j], hi4), c4, v[j]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c8, "row_ror:8");
+    const float sc = (__builtin_popcount(lane & 15) & 1) ? -kHadScale : kHadScale;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * sc;
+}
+
+// 8 consecutive halves at p (16-byte aligned: one load; else eight)
+__device__ __forceinline__ void load8h(const uint16_t* p, bool wide, uint16_t (&h)[8]) {
+    if (wide) {
+        const uint4 q = *(const uint4*)p;
+        const uint32_t w[4] = { q.x, q.y, q.z, q.w };
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = ldg16(p, j);
+    }
+}
+
+// The rotation into scratch, one wave per sorted row, 8 consecutive elements a lane: a pass covers 4 128-blocks of
+// each half (one 16-byte load of x, one of each scale and one store a half a lane), and the loads of up to ROT_PASSES
+// passes go out together: gate_up's xr (halves 0 and 1 from the same token row: suh, suh1 of the row's expert) or
+// down's rotated h (one half: down's suh, sorted rows in). The rows are dealt to the XCDs in contiguous ranges, so a
+// run's rows (one expert's scales) share an L2. Rows no run holds are not written (nothing reads them); a negative
+// sorted_tok gives zeros.
+constexpr int ROT_PASSES = 2;
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int nwg = (a.T + 3) / 4, per_xcd = (nwg + 7) / 8;
+    const int wg = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    const int i = wg * 4 + (int)(threadIdx.x >> 6);
+    if (wg >= nwg || i >= a.T) return;
     const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
-    if (wid >= (int64_t)a.T * halves) return;
-    const int64_t i = wid / halves;
-    const int m = (int)(wid % halves);
     const int e = a.row_info[2 * i];
+    const int tok = a.sorted[i];
     if (e < 0) return;
     const Exl3c4Class& K = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
     const int C = K.cols;
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C;
-    const int tok = a.sorted[i];
+    uint16_t* out = (uint16_t*)a.y + (int64_t)i * a.y_pitch;
+    const int npass = (C / 128 + 3) / 4;
     if (tok < 0) {
-        for (int b = 0; b < C / 128; ++b) {
-            out[b * 128 + lane] = 0;
-            out[b * 128 + lane + 64] = 0;
+        for (int p = 0; p < npass * halves; ++p) {
+            const int col = (p % npass) * 512 + 8 * lane;
+            if (col < C) *(uint4*)(out + (p / npass) * C + col) = uint4{ 0, 0, 0, 0 };
         }
         return;
     }
     int64_t src = halves == 2 ? tok / a.top_k : i;
     src = src < a.x_rows ? src : a.x_rows - 1;
-    const void* x = (const uint16_t*)a.x + src * a.x_pitch;
-    const void* sc = m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch;
+    const uint16_t* s0 = (const uint16_t*)tab_entry(K.suh, K.suh_stride, jx);
+    const uint16_t* s1 = halves == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_stride, jx) : s0;
+    const bool xw = (((uintptr_t)a.x | (uintptr_t)(a.x_pitch * 2)) & 15) == 0;
+    const bool sw = (((uintptr_t)s0 | (uintptr_t)s1) & 15) == 0;
     const bool bf = halves == 2 && a.x_dtype == EXL3C4_BF16;
-    // two blocks a step: the next block's four loads are out while this one rotates
-    uint16_t x0 = ldg16(x, lane), x1 = ldg16(x, 64 + lane), s0 = ldg16(sc, lane), s1 = ldg16(sc, 64 + lane);
-    for (int b = 0; b < C / 128; ++b) {
-        uint16_t nx0 = 0, nx1 = 0, ns0 = 0, ns1 = 0;
-        if (b + 1 < C / 128) {
-            const int nb0 = (b + 1) * 128;
-            nx0 = ldg16(x, nb0 + lane); nx1 = ldg16(x, nb0 + 64 + lane);
-            ns0 = ldg16(sc, nb0 + lane); ns1 = ldg16(sc, nb0 + 64 + lane);
+    for (int p0 = 0; p0 < npass; p0 += ROT_PASSES) {
+        uint16_t xh[ROT_PASSES][8], sh[2][ROT_PASSES][8];
+#pragma unroll
+        for (int q = 0; q < ROT_PASSES; ++q) {
+            int col = (p0 + q) * 512 + 8 * lane;
+            col = col < C ? col : 8 * (lane & 15);                   // past the row: reload the first block (unused)
+            load8h(x + col, xw, xh[q]);
+            load8h(s0 + col, sw, sh[0][q]);
+            if (halves == 2) load8h(s1 + col, sw, sh[1][q]);
         }
-        uint16_t o0, o1;
-        rotate_block(bf ? bf2f(x0) : h2f(x0), bf ? bf2f(x1) : h2f(x1), s0, s1, lane, o0, o1);
-        out[b * 128 + lane] = o0;
-        out[b * 128 + lane + 64] = o1;
-        x0 = nx0; x1 = nx1; s0 = ns0; s1 = ns1;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            if (m >= halves) break;
+#pragma unroll
+            for (int q = 0; q < ROT_PASSES; ++q) {
+                if (p0 + q >= npass) break;
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = h2f(f2h((bf ? bf2f(xh[q][j]) : h2f(xh[q][j])) * h2f(sh[m][q][j])));
+                had128_x8(v, lane);
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) o[j] = (uint32_t)f2h(v[2 * j]) | ((uint32_t)f2h(v[2 * j + 1]) << 16);
+                const int col = (p0 + q) * 512 + 8 * lane;
+                if (col < C) *(uint4*)(out + m * C + col) = uint4{ o[0], o[1], o[2], o[3] };
+            }
+        }
+    }
+}
+
+// gate_up's epilogue on the prefill path (one split of sums), one wave per (sorted row, group of 4 h-blocks): every
+// load of the group first (the sums of 4 gate and 4 up columns a lane a block, svh, dn_suh), then the math. A row no
+// run holds, a negative sorted_tok and a narrower class's tail are written zero.
+__global__ __launch_bounds__(256) void k_gepi_pf(const Exl3c4Launch a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int ngrp = (a.nblk + 3) / 4;
+    if (wid >= (int64_t)a.T * ngrp) return;
+    const int64_t i = wid / ngrp;
+    const int b0 = (int)(wid % ngrp) * 4;
+    const int e = a.row_info[2 * i];
+    const int c = e >= 0 ? class_of(a, e) : 0;
+    const Exl3c4Class& K = a.cls[c];
+    const int width = K.rows / 2;
+    const bool dead = e < 0 || a.sorted[i] < 0;
+    const int64_t jx = e >= 0 ? entry_of(a, e) : 0;
+    const __attribute__((address_space(1))) float* p =
+        (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
+    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
+    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    float acc[4][4];
+    uint16_t sv[4][4], dv[4][2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int b = b0 + q;
+        const bool live = !dead && b * 128 < width;
+        const int n0 = (live ? b : 0) * 128 + lane, n1 = n0 + 64;   // loads of a live block only
+        if (live) {
+            acc[q][0] = p[n0];
+            acc[q][1] = p[n1];
+            acc[q][2] = p[width + n0];
+            acc[q][3] = p[width + n1];
+            sv[q][0] = ldg16(svh, n0);
+            sv[q][1] = ldg16(svh, n1);
+            sv[q][2] = ldg16(svh, width + n0);
+            sv[q][3] = ldg16(svh, width + n1);
+            dv[q][0] = a.h_rot ? ldg16(ds, n0) : 0;
+            dv[q][1] = a.h_rot ? ldg16(ds, n1) : 0;
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int b = b0 + q;
+        if (b >= a.nblk) break;
+        uint16_t v0 = 0, v1 = 0;
+        if (!dead && b * 128 < width)
+            gate_up_math(acc[q], sv[q][0], sv[q][1], sv[q][2], sv[q][3], dv[q][0], dv[q][1], a.h_rot, lane, v0, v1);
+        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
+        out[lane] = v0;
+        out[lane + 64] = v1;
     }
 }
 
@@ -970,6 +1095,16 @@ __device__ __forceinline__ void stage_store(uint16_t* A, int kp, int nrows, cons
     }
 }
 
+// The prefill GEMMs' workgroups of one chunk share one XCD: linear id g = 8 (per q + u) + x runs unit u (0 .. per-1:
+// the chunk's column groups or blocks) of chunk 8 q + x. The dispatcher deals workgroups to the XCDs in turn, so a
+// chunk's units run side by side in one L2, and its staged rows come from HBM once, not once a unit. (Where a
+// workgroup lands changes no bits.)
+__device__ __forceinline__ void xcd_unit(int per, int& unit, int& chunk) {
+    const int g = (int)blockIdx.x, slot = g >> 3;
+    unit = slot % per;
+    chunk = (slot / per) * 8 + (g & 7);
+}
+
 // The prefill GEMM of one chunk (<= 64 rows of one expert) against one 128-column group of the weight (4 waves = 4
 // strips), all of k: the input's 128-k blocks stream through two LDS buffers; each wave decodes its strip's step once
 // and runs it against every row tile. Accumulations: acc[row tile][strip half].
@@ -1028,7 +1163,8 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
-    const int grp = blockIdx.x, chunk = blockIdx.y;
+    int grp, chunk;
+    xcd_unit(a.n_grp, grp, chunk);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = min(a.plan[0], a.max_chunks);
     if (chunk >= nch) return;
@@ -1063,7 +1199,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
-    const int b = blockIdx.x, chunk = blockIdx.y;
+    int b, chunk;
+    xcd_unit(a.nblk, b, chunk);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = min(a.plan[0], a.max_chunks);
     if (chunk >= nch) return;
@@ -1289,10 +1426,16 @@ extern "C" int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0
     return go(k_rowinfo, (unsigned)((a->T + 255) / 256), (hipStream_t)stream, ev0, ev1, *a);
 }
 
-extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->T * a->h_from_gu;
+extern "C" int exl3c4_dev_gepi_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    const int64_t waves = (int64_t)a->T * ((a->nblk + 3) / 4);
     if (waves <= 0) return 0;
-    return go(k_rot, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+    return go(k_gepi_pf, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+}
+
+extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
+    if (a->T <= 0) return 0;
+    const unsigned nwg = (unsigned)((a->T + 3) / 4);
+    return go(k_rot, 8 * ((nwg + 7) / 8), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 extern "C" int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
@@ -1305,14 +1448,14 @@ extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->n_grp <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3((unsigned)a->n_grp, (unsigned)a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
+    return go2(f, dim3((unsigned)(8 * a->n_grp * ((a->max_chunks + 7) / 8))), (hipStream_t)stream, ev0, ev1, 0u, *a);
 }
 
 extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const GemmFn f = by_bits<DnPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3((unsigned)a->nblk, (unsigned)a->max_chunks), (hipStream_t)stream, ev0, ev1, 0u, *a);
+    return go2(f, dim3((unsigned)(8 * a->nblk * ((a->max_chunks + 7) / 8))), (hipStream_t)stream, ev0, ev1, 0u, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

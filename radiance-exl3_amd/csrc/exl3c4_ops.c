@@ -339,8 +339,7 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
         a.h_rot = op == EXL3C4_GU_DN ? 1 : o->h_rot;
         if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
         else a.nblk = (int32_t)(o->y_cols / 128);
-        a.blk_per_wave = a.nblk;                  /* a wave a row: many rows, no need to spread a row's blocks */
-        if ((rc = exl3c4_dev_gepi(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
+        if ((rc = exl3c4_dev_gepi_pf(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
         if (op == EXL3C4_GATE_UP) return EXL3C4_OK;
         din = s + k->h;
         din_pitch = k->h_pitch;
