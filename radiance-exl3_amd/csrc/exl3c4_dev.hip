@@ -266,6 +266,17 @@ __device__ __forceinline__ half8_t as_half8(uint32_t a, uint32_t b, uint32_t c, 
     return __builtin_bit_cast(half8_t, u32x4_t{ a, b, c, d });
 }
 
+// gfx950's v_mfma_f32_16x16x32_f16 still reads its A and B registers for some cycles after it issues, and the compiler
+// does not hold back a VALU or load that writes them meanwhile (measured: an address computed into a just-issued MFMA's
+// B registers corrupted the product). Every group of MFMAs ends with this guard: the scheduler may move nothing across
+// it, and its inputs keep the group's operand registers allocated through 16 wait states after the last MFMA.
+__device__ __forceinline__ void mfma_guard(const half8_t& a0, const half8_t& a1, const half8_t& b0, const half8_t& b1,
+                                           const half8_t& b2, const half8_t& b3) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_nop 7\n\ts_nop 7" ::"v"(a0), "v"(a1), "v"(b0), "v"(b1), "v"(b2), "v"(b3));
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 // ------------------------------------------------------------------------------------------------ kernels
 
 // The order of k inside every 16-group of an activation row stored PERMUTED: position p holds k = kPerm[p], so that one
@@ -472,10 +483,13 @@ __device__ __forceinline__ void mma_step(const uint32_t (&d)[BITS], const uint16
     decode_segment<BITS, CB>(d, B, k);
     const half8_t Aa = *(const half8_t*)(arow);
     const half8_t Ab = *(const half8_t*)(arow + 8);
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[0], B[1], B[2], B[3]), acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, as_half8(B[8], B[9], B[10], B[11]), acc1, 0, 0, 0);
-    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[4], B[5], B[6], B[7]), acc0, 0, 0, 0);
-    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, as_half8(B[12], B[13], B[14], B[15]), acc1, 0, 0, 0);
+    const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
+    const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b0, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b1, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, b2, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ab, b3, acc1, 0, 0, 0);
+    mfma_guard(Aa, Ab, b0, b1, b2, b3);
 }
 
 // The codes of the next PF steps of a wave's stream: in flight while the earlier steps are decoded.
@@ -497,13 +511,15 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r
                                            float4_t& acc0, float4_t& acc1) {
     const Mul1Consts k = mul1_consts();
     constexpr int PF = EXL3C4_GEMV_PF;
+    // ksn is even (two steps a 128-block) and PF two, so both steps of a pair exist; the refill is unconditional (past
+    // the stream a harmless reload of the last step), so the waits for the codes are counted, not drained
+    static_assert(PF == 2, "gemv_strip runs its steps in pairs");
     for (int s = 0; s < ksn; s += PF) {
 #pragma unroll
         for (int q = 0; q < PF; ++q) {
-            if (s + q < ksn) {
-                mma_step<BITS, CB>(r.d[q], arow + (s + q) * EXL3C4_KSTEP, k, acc0, acc1);
-                if (s + q + PF < ksn) load_words<BITS>(rec + (s + q + PF) * 64 * BITS, r.d[q]);
-            }
+            mma_step<BITS, CB>(r.d[q], arow + (s + q) * EXL3C4_KSTEP, k, acc0, acc1);
+            const int nx = s + q + PF < ksn ? s + q + PF : ksn - 1;
+            load_words<BITS>(rec + nx * 64 * BITS, r.d[q]);
         }
     }
 }
@@ -1135,8 +1151,11 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
             const int ks = 2 * kb + s;
             uint32_t B[16];
             decode_segment<BITS, CB>(s ? dB : dA, B, k);
-            if (s == 0 && ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dA);
-            if (s == 1 && ks + 2 < ksteps) load_words<BITS>(rec + (ks + 2) * 64 * BITS, dB);
+            // the step two ahead, or past the stream a harmless reload of the last: unconditional, so the waits for
+            // the codes are counted, not drained
+            const int nx = ks + 2 < ksteps ? ks + 2 : ksteps - 1;
+            if (s == 0) load_words<BITS>(rec + nx * 64 * BITS, dA);
+            else load_words<BITS>(rec + nx * 64 * BITS, dB);
             const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
             const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
 #pragma unroll
@@ -1148,6 +1167,7 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
                     acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b1, acc[t][1], 0, 0, 0);
                     acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b2, acc[t][0], 0, 0, 0);
                     acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b3, acc[t][1], 0, 0, 0);
+                    mfma_guard(Aa, Ac, b0, b1, b2, b3);
                 }
             }
         }
