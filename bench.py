@@ -200,21 +200,23 @@ def run_decode_layer(args, torch, exl3c4):
         ops.append(exl3c4.make_op(exl3c4.GU_DN, BITS, CB, [L["gu_cls"]], D["x"], D["sorted_tok"], D["off"], y, M,
                                   TOP_K, dn=[L["dn_cls"]]))
     scratch = exl3c4.alloc_scratch(ops[0])
+    # gate_up_down's counter block: zeroed once here, left zeroed by every launch (exl3c4_launch_ctr)
+    ctr = torch.zeros(max(exl3c4.ctr_bytes(ops[0]), 256), dtype=torch.uint8, device="cuda")
 
     def layer_step(i, stream):
         D = draws[i % n % args.draws]
         check_rc(exl3c4, exl3c4.router_topk_scatter(D["logits"], TOP_K, True, ids, w, st_d, off_d, None, row_of,
                                                     stream))
-        check_rc(exl3c4, exl3c4.launch(layer_ops[i % n], scratch, stream))
+        check_rc(exl3c4, exl3c4.launch_ctr(layer_ops[i % n], scratch, ctr, stream))
         check_rc(exl3c4, exl3c4.moe_gather(y, True, w, row_of, out_t, stream))
     ms = timed_graph(torch, layer_step, args.steps, args.warmup)
-    ms_op = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch(ops[i % n], scratch, st)),
+    ms_op = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch_ctr(ops[i % n], scratch, ctr, st)),
                         args.steps, args.warmup)
     ms_step = ms / args.steps
     live = [draws[i % n % args.draws]["n_live"] for i in range(args.steps)]
-    st = exl3c4.launch_status(ops[0], scratch)
-    if st:
-        raise RuntimeError(f"gate_up_down's single kernel left status {st}")
+    st = int(ctr[:4].cpu().numpy().view(np.int32)[0])
+    if st or int(torch.count_nonzero(ctr)):
+        raise RuntimeError(f"gate_up_down's single kernel left status {st} or a nonzero counter block")
     layer_gbps = float(np.mean(live)) * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
     one = T >= exl3c4.GD_FUSE_MIN_T           # gate_up_down runs as one kernel: that kernel is the one timed
     durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP_DOWN if one else exl3c4.K_GATE_UP, args.steps)

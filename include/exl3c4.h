@@ -113,6 +113,20 @@ int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* ro
  * before every refusal has been decided. `scratch` is device memory of at least exl3c4_scratch_bytes, 256-B aligned. */
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
+/* gate_up_down's single kernel (the decode path from EXL3C4_GD_FUSE_MIN_T sorted rows) orders its workgroups through
+ * a block of counters -- a status word and two counters a sorted row -- that must be zero when it starts and that it
+ * leaves zero again when it ends well (each row's last down unit zeroes the row's). exl3c4_launch zeroes them in its
+ * scratch before every launch (one more dispatch). exl3c4_launch_ctr takes them from `ctr` instead: a device block of
+ * at least exl3c4_ctr_bytes, 256-B aligned, that the caller zeroed once (hipMemset) and keeps -- the reference's
+ * counter pool, which its row instance's init allocates and zeroes and whose blocks the fused launch leaves zero
+ * (kernels/exl3r4d/launch.c:311-324; the fused launch's `ctr` argument, launch.c:464-466). The block's first int32 is
+ * the status word exl3c4_scratch_status describes (0: good); after a launch that left it nonzero, zero the block again.
+ * Two launches that may overlap (two streams) need two blocks; launches that share one are ordered on one stream. A
+ * launch that does not run that kernel does not read ctr: exl3c4_launch_ctr is then exl3c4_launch. */
+int64_t exl3c4_ctr_bytes(const Exl3c4Op* op);
+int exl3c4_launch_ctr(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                      int64_t ctr_bytes);
+
 /* The kernels a launch can run: prep_gu's rotation; gate_up's GEMM (with its input rotation), then for gate_up alone
  * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums); and
  * gate_up_down's single kernel, which runs both GEMMs in one dispatch at decode once T >= EXL3C4_GD_FUSE_MIN_T.

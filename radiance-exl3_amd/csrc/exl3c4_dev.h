@@ -17,8 +17,10 @@ extern "C" {
 /* Columns one wave's strip holds (two 16-column tiles) and k one step consumes (four 16-k tiles). */
 #define EXL3C4_STRIP 32
 #define EXL3C4_KSTEP 64
-/* int32 words between two row counters of gate_up_down's single kernel (256 B: each counter its own cache line) */
+/* int32 words between two row counters of gate_up_down's single kernel (256 B: each counter its own cache line), and
+ * where in a row's line the count of its down units past their wait sits */
 #define EXL3C4_SYNC_STRIDE 64
+#define EXL3C4_SYNC_DONE 32
 /* Rows of one chunk on the prefill path (four MFMA row tiles decode-shared). */
 #define EXL3C4_PF_ROWS 64
 

@@ -631,7 +631,8 @@ __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
     }
 }
 
-// Row i's counter: each in its own cache line, so that polls and counts of different rows do not meet.
+// Row i's counter: each in its own cache line, so that polls and counts of different rows do not meet. Half a line on,
+// EXL3C4_SYNC_DONE words in, the count of the row's down units past their wait.
 __device__ __forceinline__ int32_t* row_counter(const Exl3c4Launch& a, int i) {
     return a.sync + (int64_t)(i + 1) * EXL3C4_SYNC_STRIDE;
 }
@@ -712,7 +713,18 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     const void* svh = tab_entry(D.svh, D.svh_stride, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_stride, jx) : nullptr;
-    if (FUSED) wait_gate_up(a, i);
+    if (FUSED) {
+        wait_gate_up(a, i);
+        // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the
+        // row's counters, so a launch leaves them as it found them (the reference's counter blocks,
+        // kernels/exl3r4d/launch.c:311-324)
+        if (threadIdx.x == 0 &&
+            __hip_atomic_fetch_add(row_counter(a, i) + EXL3C4_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                N / 128 - 1) {
+            __hip_atomic_store(row_counter(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(row_counter(a, i) + EXL3C4_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 
     // stage the chunk's rows
     const int nhb = KC / 128;

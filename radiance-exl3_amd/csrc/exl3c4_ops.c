@@ -355,9 +355,9 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     return exl3c4_dev_zero_dead(&d, stream, NULL, NULL);
 }
 
-/* gate_up_down at decode as one kernel: the row counters and status zeroed, then k_gd (gate_up units, then down
- * units waiting on their row's counter). */
-static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t) {
+/* gate_up_down at decode as one kernel: the row counters and status zeroed (or the caller's zeroed block taken), then
+ * k_gd (gate_up units, then down units waiting on their row's counter; the row's last down unit zeroes its counters). */
+static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t, int32_t* ctr) {
     int rc;
     Exl3c4Launch g;
     base_args(o, k, s, &g);
@@ -371,10 +371,14 @@ static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, 
     g.nblk = (int32_t)(o->y_cols / 128);
     g.dacc = (float*)(s + k->dacc);
     g.dacc_pitch = k->dacc_pitch;
-    g.sync = (int32_t*)(s + k->sync);
     g.hbuf = (uint16_t*)(s + k->h);
     g.hbuf_pitch = k->h_pitch;
-    if ((rc = exl3c4_dev_fill(g.sync, (o->T + 1) * EXL3C4_SYNC_STRIDE, stream)) != 0) return rc;
+    if (ctr) {                                    /* the caller's counter block: zero, and left zero */
+        g.sync = ctr;
+    } else {
+        g.sync = (int32_t*)(s + k->sync);
+        if ((rc = exl3c4_dev_fill(g.sync, (o->T + 1) * EXL3C4_SYNC_STRIDE, stream)) != 0) return rc;
+    }
     return exl3c4_dev_gd(&g, stream, EV(EXL3C4_K_GATE_UP_DOWN));
 }
 
@@ -401,7 +405,8 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
  *   down          its GEMM, whose workgroups stage (and rotate) their rows and finish their output blocks
  *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums; from
  *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1) */
-static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t) {
+static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t,
+                       int32_t* ctr) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     if ((rc = check(o)) != EXL3C4_OK) return rc;
@@ -420,7 +425,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     }
 
     if (k.pf) return launch_prefill(o, &k, s, stream, t);
-    if (k.gd1) return launch_gd1(o, &k, s, stream, t);
+    if (k.gd1) return launch_gd1(o, &k, s, stream, t, ctr);
 
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
@@ -459,7 +464,31 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
 
 int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
     const Timed t = { -1, NULL, NULL };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
+}
+
+int64_t exl3c4_ctr_bytes(const Exl3c4Op* o) {
+    Exl3c4Op q;
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    q = *o;
+    q.T = o->M * o->top_k;
+    if ((rc = check(&q)) != EXL3C4_OK) return rc;
+    const int64_t T = q.T > o->T ? q.T : o->T;
+    return q.op == EXL3C4_GU_DN ? ALIGN_UP((T + 1) * EXL3C4_SYNC_STRIDE * 4, 256) : 0;
+}
+
+int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                      int64_t ctr_bytes) {
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    Carve k;
+    carve(o, o->T, &k);
+    if (k.gd1 && ctr && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
+        return EXL3C4_E_SCRATCH;
+    const Timed t = { -1, NULL, NULL };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL);
 }
 
 int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
@@ -471,7 +500,7 @@ int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes,
     carve(o, o->T, &k);
     if (!runs_kernel(o, &k, kernel)) return EXL3C4_E_INVAL;
     const Timed t = { kernel, ev_start, ev_stop };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
 }
 
 int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,

@@ -76,6 +76,10 @@ def lib():
         L.exl3c4_router_topk_scatter.argtypes = [_p, _i32, _i64, _i64, _i64, _i32, _i32, _p, _p, _p, _p, _p, _p, _p]
         L.exl3c4_moe_gather.restype = C.c_int
         L.exl3c4_moe_gather.argtypes = [_p, _i32, _i64, _p, _p, _i64, _i32, _i64, _p, _i64, _p]
+        L.exl3c4_ctr_bytes.restype = _i64
+        L.exl3c4_ctr_bytes.argtypes = [C.POINTER(Op)]
+        L.exl3c4_launch_ctr.restype = C.c_int
+        L.exl3c4_launch_ctr.argtypes = [C.POINTER(Op), _p, _i64, _p, _p, _i64]
         L.exl3c4_scratch_status.restype = C.c_int
         L.exl3c4_scratch_status.argtypes = [C.POINTER(Op), C.POINTER(_i64)]
         L.exl3c4_build_target.restype = C.c_char_p
@@ -223,6 +227,18 @@ def launch(o: Op, scratch=None, stream=None) -> int:
     """Runs one op; returns the status (0 OK). `scratch`: a uint8 device tensor of >= scratch_bytes(o)."""
     n = 0 if scratch is None else scratch.numel()
     return int(lib().exl3c4_launch(C.byref(o), _ptr(scratch), n, _stream(stream)))
+
+
+def ctr_bytes(o: Op) -> int:
+    """Bytes of the counter block exl3c4_launch_ctr takes for `o` (0: the op keeps no counters)."""
+    return int(lib().exl3c4_ctr_bytes(C.byref(o)))
+
+
+def launch_ctr(o: Op, scratch, ctr, stream=None) -> int:
+    """exl3c4_launch_ctr: `ctr` a zeroed uint8 device tensor of >= ctr_bytes(o) bytes, 256-B aligned; left zeroed."""
+    n = 0 if scratch is None else scratch.numel()
+    m = 0 if ctr is None else ctr.numel()
+    return int(lib().exl3c4_launch_ctr(C.byref(o), _ptr(scratch), n, _stream(stream), _ptr(ctr), m))
 
 
 def partial_sums(o: Op, scratch, gemm: int = 0):

@@ -228,3 +228,33 @@ def test_single_routed_expert_at_the_baseline_geometry(torch_cuda, bits, m):
     h1 = dev.gate_up(h_rot=1)
     assert np.array_equal(h1, case.h_rot_of(h0))
     assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
+
+
+# ------------------------------------------------------------------------------------------ the caller's counter block
+def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bits(torch_cuda):
+    """exl3c4_launch_ctr: gate_up_down's single kernel takes its counters from a block the caller zeroed once; after
+    every launch the block is zero again (each row's last down unit zeroes the row's counters) and the output is the
+    bits of exl3c4_launch, which zeroes counters in scratch itself. Several launches in a row on one block, with
+    different routing draws and row counts."""
+    import exl3c4 as ex
+    torch = torch_cuda
+    ctr = None
+    for seed, n_tok, top_k, n_expert in ((70, 8, 10, 96), (71, 6, 8, 40), (72, 8, 10, 96), (73, 4, 8, 12)):
+        case = Case(seed=seed, n_tok=n_tok, top_k=top_k, n_expert=n_expert, geoms=[(512, 256)], bits=4, cb="mul1",
+                    drop=0.05)
+        dev = Dev(case)
+        want = dev.gate_up_down()
+        assert dev.status == 0
+        N = max(d["rows"] for d in dev.tabs["dn"])
+        y = dev.out(N, fill=0x1234)
+        dn = [ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in dev.tabs["dn"]]
+        o = ex.make_op(ex.GU_DN, case.bits, case.cb, dev.cls("gu"), dev.x, dev.sorted_tok, dev.off, y, 8, case.top_k,
+                       dn=dn)
+        assert case.T >= ex.GD_FUSE_MIN_T and ex.ctr_bytes(o) > 0
+        if ctr is None:
+            ctr = torch.zeros(max(ex.ctr_bytes(o), 256), dtype=torch.uint8, device="cuda")
+        s = ex.alloc_scratch(o)
+        assert ex.launch_ctr(o, s, ctr) == 0
+        torch.cuda.synchronize()
+        assert int(torch.count_nonzero(ctr)) == 0, f"seed {seed}: the counter block is not zero after the launch"
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
