@@ -71,7 +71,6 @@ int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream);
 int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
-int exl3c4_dev_gepi_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);

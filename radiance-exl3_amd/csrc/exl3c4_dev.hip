@@ -1010,59 +1010,6 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     }
 }
 
-// gate_up's epilogue on the prefill path (one split of sums), one wave per (sorted row, group of 4 h-blocks): every
-// load of the group first (the sums of 4 gate and 4 up columns a lane a block, svh, dn_suh), then the math. A row no
-// run holds, a negative sorted_tok and a narrower class's tail are written zero.
-__global__ __launch_bounds__(256) void k_gepi_pf(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int ngrp = (a.nblk + 3) / 4;
-    if (wid >= (int64_t)a.T * ngrp) return;
-    const int64_t i = wid / ngrp;
-    const int b0 = (int)(wid % ngrp) * 4;
-    const int e = a.row_info[2 * i];
-    const int c = e >= 0 ? class_of(a, e) : 0;
-    const Exl3c4Class& K = a.cls[c];
-    const int width = K.rows / 2;
-    const bool dead = e < 0 || a.sorted[i] < 0;
-    const int64_t jx = e >= 0 ? entry_of(a, e) : 0;
-    const __attribute__((address_space(1))) float* p =
-        (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
-    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
-    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
-    float acc[4][4];
-    uint16_t sv[4][4], dv[4][2];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int b = b0 + q;
-        const bool live = !dead && b * 128 < width;
-        const int n0 = (live ? b : 0) * 128 + lane, n1 = n0 + 64;   // loads of a live block only
-        if (live) {
-            acc[q][0] = p[n0];
-            acc[q][1] = p[n1];
-            acc[q][2] = p[width + n0];
-            acc[q][3] = p[width + n1];
-            sv[q][0] = ldg16(svh, n0);
-            sv[q][1] = ldg16(svh, n1);
-            sv[q][2] = ldg16(svh, width + n0);
-            sv[q][3] = ldg16(svh, width + n1);
-            dv[q][0] = a.h_rot ? ldg16(ds, n0) : 0;
-            dv[q][1] = a.h_rot ? ldg16(ds, n1) : 0;
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int b = b0 + q;
-        if (b >= a.nblk) break;
-        uint16_t v0 = 0, v1 = 0;
-        if (!dead && b * 128 < width)
-            gate_up_math(acc[q], sv[q][0], sv[q][1], sv[q][2], sv[q][3], dv[q][0], dv[q][1], a.h_rot, lane, v0, v1);
-        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
-        out[lane] = v0;
-        out[lane + 64] = v1;
-    }
-}
-
 // Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows).
 __global__ __launch_bounds__(256) void k_zero_dead(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
@@ -1096,10 +1043,11 @@ __global__ __launch_bounds__(256) void k_rowinfo(const Exl3c4Launch a) {
 // the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` are not loaded.
 struct StageRegs { u32x4_t v[4]; };
 __device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, int row0, int nrows, int col0,
-                                           StageRegs& r) {
+                                           StageRegs& r, int tid = -1) {
+    if (tid < 0) tid = (int)threadIdx.x;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int g = (int)threadIdx.x + 256 * h;                // 512 groups: row g / 8, 16-group g % 8
+        const int g = tid + 256 * h;                              // 512 groups: row g / 8, 16-group g % 8
         const int q = g >> 3, grp = g & 7;
         if (q < nrows) {
             const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
@@ -1109,10 +1057,11 @@ __device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, i
         }
     }
 }
-__device__ __forceinline__ void stage_store(uint16_t* A, int kp, int nrows, const StageRegs& r) {
+__device__ __forceinline__ void stage_store(uint16_t* A, int kp, int nrows, const StageRegs& r, int tid = -1) {
+    if (tid < 0) tid = (int)threadIdx.x;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const int g = (int)threadIdx.x + 256 * h;
+        const int g = tid + 256 * h;
         const int q = g >> 3, grp = g & 7;
         if (q < nrows) {
             const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
@@ -1133,31 +1082,35 @@ __device__ __forceinline__ void xcd_unit(int per, int& unit, int& chunk) {
     chunk = (slot / per) * 8 + (g & 7);
 }
 
-// The prefill GEMM of one chunk (<= 64 rows of one expert) against one 128-column group of the weight (4 waves = 4
-// strips), all of k: the input's 128-k blocks stream through two LDS buffers; each wave decodes its strip's step once
-// and runs it against every row tile. Accumulations: acc[row tile][strip half].
-template <int BITS, int CB>
+// The prefill GEMM of one chunk (<= 64 rows of one expert) against the strips of one workgroup, all of k: the input's
+// 128-k blocks stream through two LDS buffers a half; each wave decodes its strip's step once and runs it against every
+// row tile. NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8 waves, two staged inputs (columns k
+// and half_off + k), thread t staging half t / 256 and wave w reading half w / 4. Accumulations: acc[row tile][strip
+// half].
+template <int BITS, int CB, int NH>
 __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
-                                        uint16_t* lds, float4_t (&acc)[4][2]) {
+                                        int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
     const int lane = threadIdx.x & 63;
     const int KC = W.cols, nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
     const int kp = 128 + 8;
-    uint16_t* buf[2] = { lds, lds + 64 * kp };
+    const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
+    const int scol = col_off + sh * half_off;                     // this thread's staged input column
+    auto bufp = [&](int b, int h) { return lds + (b * NH + h) * 64 * kp; };
     const int ntile = (nrows + 15) >> 4;
     const gu32p rec = (gu32p)tab_entry(W.codes, W.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     uint32_t dA[BITS], dB[BITS];
     load_words<BITS>(rec, dA);
     load_words<BITS>(rec + 64 * BITS, dB);
     StageRegs r;
-    stage_load(src, pitch, row0, nrows, col_off, r);
-    stage_store(buf[0], kp, nrows, r);
+    stage_load(src, pitch, row0, nrows, scol, r, tid);
+    stage_store(bufp(0, sh), kp, nrows, r, tid);
     __syncthreads();
     const Mul1Consts k = mul1_consts();
     const int rr = lane & 15, g = lane >> 4;
     for (int kb = 0; kb < nb; ++kb) {
-        if (kb + 1 < nb) stage_load(src, pitch, row0, nrows, col_off + (kb + 1) * 128, r);
-        const uint16_t* Ab = buf[kb & 1];
+        if (kb + 1 < nb) stage_load(src, pitch, row0, nrows, scol + (kb + 1) * 128, r, tid);
+        const uint16_t* Ab = bufp(kb & 1, sh);
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int ks = 2 * kb + s;
@@ -1184,35 +1137,50 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
             }
         }
         if (kb + 1 < nb) {
-            stage_store(buf[(kb + 1) & 1], kp, nrows, r);
+            stage_store(bufp((kb + 1) & 1, sh), kp, nrows, r, tid);
         }
         __syncthreads();
     }
 }
 
-// gate_up's prefill GEMM: one workgroup per (chunk, 128-column group); xr (prep_gu's rows, sorted-row order) in, the f32
-// sums of the chunk's rows out to part (one split): the epilogue kernel finishes them.
+// gate_up's prefill GEMM with its epilogue: one workgroup of 8 waves per (chunk, h-block hb): waves 0..3 the 4 gate
+// strips of columns 128 hb .., waves 4..7 the 4 up strips of columns N / 2 + 128 hb .., each half of xr staged for
+// its waves. The raw sums go to part (a checker's view); then the accumulations cross LDS and each wave finishes whole
+// rows of the block: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh)))
+// (kernels/exl3ref/ref.c:187-212) into y at columns 128 hb... A negative sorted_tok, and a narrower class's blocks past
+// its width, are written zero; rows no run holds are k_zero_dead's.
 template <int BITS, int CB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
-    int grp, chunk;
-    xcd_unit(a.n_grp, grp, chunk);
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
+    constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
+    int hb, chunk;
+    xcd_unit(a.n_grp / 2, hb, chunk);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nch = min(a.plan[0], a.max_chunks);
     if (chunk >= nch) return;
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
     const Exl3c4Class& K = a.cls[class_of(a, e)];
-    const int N = K.rows, KC = K.cols;
-    if (grp * 128 >= N) return;
-    const bool up = grp * 128 >= N / 2;
+    const int64_t jx = entry_of(a, e);
+    const int N = K.rows, KC = K.cols, width = N / 2;
+    if (hb * 128 >= width) {                                      // a narrower class: its rows' block past its width
+        if (hb < a.nblk)
+            for (int q = wave; q < nrows; q += 8) {
+                uint16_t* out = (uint16_t*)a.y + (int64_t)(row0 + q) * a.y_pitch + hb * 128;
+                out[lane] = 0;
+                out[lane + 64] = 0;
+            }
+        return;
+    }
+    const int half = wave >> 2, strip = half ? N / 64 + 4 * hb + (wave & 3) : 4 * hb + wave;
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-    pf_gemm<BITS, CB>(a, K, entry_of(a, e), grp * 4 + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows,
-                      up ? KC : 0, lds, acc);
+    pf_gemm<BITS, CB, 2>(a, K, jx, strip, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, KC, lds, acc);
     const int cc = lane & 15, rg = lane >> 4;
-    const int n = (grp * 4 + wave) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
+    const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
+    const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
+    float* acc_l = (float*)lds;                                   // [64][ACC_PITCH], over the staging buffers
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1221,8 +1189,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             if (row < nrows) {
                 a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
                 a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
+                acc_l[row * ACC_PITCH + col_l] = acc[t][0][q];
+                acc_l[row * ACC_PITCH + col_l + 8] = acc[t][1][q];
             }
         }
+    __syncthreads();
+    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
+    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    const int n0 = hb * 128 + lane, n1 = n0 + 64;
+    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
+    const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
+    for (int row = wave; row < nrows; row += 8) {
+        const int64_t r = row0 + row;
+        uint16_t v0 = 0, v1 = 0;
+        if (a.sorted[r] >= 0) {
+            const float* p = acc_l + row * ACC_PITCH;
+            const float ac[4] = { p[lane], p[lane + 64], p[128 + lane], p[192 + lane] };
+            gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
+        }
+        uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
+        out[lane] = v0;
+        out[lane + 64] = v1;
+    }
 }
 
 // down's prefill GEMM: one workgroup per (chunk, 128-column output block); h (rotated, sorted-row order) in; the
@@ -1252,7 +1240,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-    pf_gemm<BITS, CB>(a, D, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, lds, acc);
+    pf_gemm<BITS, CB, 1>(a, D, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0, lds, acc);
 
     const void* svh = tab_entry(D.svh, D.svh_stride, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
@@ -1458,12 +1446,6 @@ extern "C" int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0
     return go(k_rowinfo, (unsigned)((a->T + 255) / 256), (hipStream_t)stream, ev0, ev1, *a);
 }
 
-extern "C" int exl3c4_dev_gepi_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = (int64_t)a->T * ((a->nblk + 3) / 4);
-    if (waves <= 0) return 0;
-    return go(k_gepi_pf, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
-}
-
 extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     if (a->T <= 0) return 0;
     const unsigned nwg = (unsigned)((a->T + 3) / 4);
@@ -1479,8 +1461,13 @@ extern "C" int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* e
 extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
-    if (a->n_grp <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3((unsigned)(8 * a->n_grp * ((a->max_chunks + 7) / 8))), (hipStream_t)stream, ev0, ev1, 0u, *a);
+    if (a->n_grp < 2 || a->max_chunks <= 0) return 0;
+    const dim3 grid((unsigned)(8 * (a->n_grp / 2) * ((a->max_chunks + 7) / 8)));
+    if (ev0 && ev1)
+        hipExtLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, *a);
+    else
+        hipLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, *a);
+    return launched();
 }
 
 extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {

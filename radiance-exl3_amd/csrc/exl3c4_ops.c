@@ -335,12 +335,12 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
         a.x_pitch = gin_pitch;
         a.ksplit = 1;
         a.n_grp = (int32_t)(max_rows(o) / 128);
-        if ((rc = exl3c4_dev_gu_pf(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
         a.h_rot = op == EXL3C4_GU_DN ? 1 : o->h_rot;
         if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
         else a.nblk = (int32_t)(o->y_cols / 128);
-        if ((rc = exl3c4_dev_gepi_pf(&a, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
-        if (op == EXL3C4_GATE_UP) return EXL3C4_OK;
+        /* the GEMM with its epilogue: h (rotated for down when h_rot) for every row a chunk holds */
+        if ((rc = exl3c4_dev_gu_pf(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
+        if (op == EXL3C4_GATE_UP) return exl3c4_dev_zero_dead(&a, stream, NULL, NULL);
         din = s + k->h;
         din_pitch = k->h_pitch;
     }
@@ -388,7 +388,7 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
     if (op == EXL3C4_PREP_GU) return kernel == EXL3C4_K_PREP;
     if (k->pf) {
         if (kernel == EXL3C4_K_PREP) return 1;                   /* the plan */
-        if (kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_EPI_GU) return op != EXL3C4_DOWN;
+        if (kernel == EXL3C4_K_GATE_UP) return op != EXL3C4_DOWN;
         return kernel == EXL3C4_K_DOWN && op != EXL3C4_GATE_UP;
     }
     if (k->gd1) return kernel == EXL3C4_K_GATE_UP_DOWN;
