@@ -142,10 +142,17 @@ enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DO
 int exl3c4_launch_timed(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop);
 
+/* exl3c4_launch, and on the prefill path (a chunk plan: from 64 and 8 n_expert sorted rows) its GEMMs also write
+ * their f32 accumulations to scratch for exl3c4_scratch_partials -- 4 bytes a row and output column each, which the
+ * production launch does not spend. The outputs are exl3c4_launch's, bit for bit. A checker's entry; no counterpart
+ * in the reference. */
+int exl3c4_launch_checked(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
+
 /* Where a launch of `op` leaves the f32 accumulations of its GEMM (gemm 0: gate_up's, or down's for the down op; 1:
  * gate_up_down's down) in its scratch: acc[row][col] = sum over s < *splits of the f32 at scratch + *offset +
- * 4 * (s * *split_stride + row * *pitch + col), for the live rows. The epilogue adds them in this order. For a checker
- * of the accumulation itself (the values before any narrowing); no counterpart in the reference. */
+ * 4 * (s * *split_stride + row * *pitch + col), for the live rows. The epilogue adds them in this order. Every
+ * decode-path launch leaves them; a prefill-path launch only through exl3c4_launch_checked. For a checker of the
+ * accumulation itself (the values before any narrowing); no counterpart in the reference. */
 int exl3c4_scratch_partials(const Exl3c4Op* op, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,
                             int32_t* splits);
 

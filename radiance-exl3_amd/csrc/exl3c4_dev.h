@@ -56,6 +56,7 @@ typedef struct Exl3c4Launch {
     int32_t*       sync;          /* gate_up_down in one launch: a status word, then row i's counter at (i + 1) * SYNC_STRIDE */
     uint16_t*      hbuf;          /* gate_up_down in one launch: h (rotated, f16) of every chunk's rows [T][hbuf_pitch] */
     int64_t        hbuf_pitch;
+    int32_t        keep_sums;     /* prefill: also leave the GEMMs' f32 sums in part / dacc (a checker's view) */
 } Exl3c4Launch;
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the

@@ -1040,7 +1040,9 @@ __global__ __launch_bounds__(256) void k_rowinfo(const Exl3c4Launch a) {
 
 // Stage one 128-k block of up to 64 rows of a row-major f16 source into LDS, permuted (perm_slot) so that each A
 // operand is one ds_read_b128: thread t takes two 16-groups; a group's first 8 halves (k 0..7) land in dwords 0,2,4,6 of
-// the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` are not loaded.
+// the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` (>= 1) load and store a
+// copy of the last row: every thread issues the same loads, so the waits the compiler counts for the loads issued
+// before them (the codes in flight) stay exact instead of draining; those rows' products are never written.
 struct StageRegs { u32x4_t v[4]; };
 __device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, int row0, int nrows, int col0,
                                            StageRegs& r, int tid = -1) {
@@ -1048,38 +1050,39 @@ __device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, i
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int g = tid + 256 * h;                              // 512 groups: row g / 8, 16-group g % 8
-        const int q = g >> 3, grp = g & 7;
-        if (q < nrows) {
-            const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
-                (src + (int64_t)(row0 + q) * pitch + col0 + grp * 16);
-            r.v[2 * h] = p[0];
-            r.v[2 * h + 1] = p[1];
-        }
+        const int q = min(g >> 3, nrows - 1), grp = g & 7;
+        const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
+            (src + (int64_t)(row0 + q) * pitch + col0 + grp * 16);
+        r.v[2 * h] = p[0];
+        r.v[2 * h + 1] = p[1];
     }
 }
-__device__ __forceinline__ void stage_store(uint16_t* A, int kp, int nrows, const StageRegs& r, int tid = -1) {
+__device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs& r, int tid = -1) {
     if (tid < 0) tid = (int)threadIdx.x;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int g = tid + 256 * h;
         const int q = g >> 3, grp = g & 7;
-        if (q < nrows) {
-            const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
-            u32x4_t* d = (u32x4_t*)(A + q * kp + grp * 16);
-            d[0] = u32x4_t{ lo.x, hi.x, lo.y, hi.y };
-            d[1] = u32x4_t{ lo.z, hi.z, lo.w, hi.w };
-        }
+        const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
+        u32x4_t* d = (u32x4_t*)(A + q * kp + grp * 16);
+        d[0] = u32x4_t{ lo.x, hi.x, lo.y, hi.y };
+        d[1] = u32x4_t{ lo.z, hi.z, lo.w, hi.w };
     }
 }
 
-// The prefill GEMMs' workgroups of one chunk share one XCD: linear id g = 8 (per q + u) + x runs unit u (0 .. per-1:
-// the chunk's column groups or blocks) of chunk 8 q + x. The dispatcher deals workgroups to the XCDs in turn, so a
-// chunk's units run side by side in one L2, and its staged rows come from HBM once, not once a unit. (Where a
-// workgroup lands changes no bits.)
-__device__ __forceinline__ void xcd_unit(int per, int& unit, int& chunk) {
-    const int g = (int)blockIdx.x, slot = g >> 3;
-    unit = slot % per;
-    chunk = (slot / per) * 8 + (g & 7);
+// The prefill GEMMs' workgroups and XCDs: XCD x (the dispatcher deals linear ids g to the XCDs in turn, x = g % 8)
+// takes the contiguous chunks [x nq, x nq + nq) of the plan, nq = ceil(chunks / 8), its slot g / 8 = per q + u running
+// unit u (0 .. per-1: the chunk's column groups or blocks) of its q-th chunk. A chunk's units run side by side in one
+// L2, so its staged rows come from HBM once; and the plan lists an expert's chunks one after another, so they too
+// share an L2 and, running close in time, read the expert's codes from HBM about once. Every chunk costs about the
+// same (its decode), so equal ranges balance the XCDs. False for a workgroup with no chunk (the grid covers the
+// plan's bound). (Where a workgroup lands changes no bits.)
+__device__ __forceinline__ bool xcd_unit(int per, int nch, int& unit, int& chunk) {
+    const int g = (int)blockIdx.x, slot = g >> 3, x = g & 7;
+    const int nq = (nch + 7) >> 3, q = slot / per;
+    unit = slot - q * per;
+    chunk = x * nq + q;
+    return q < nq && chunk < nch;
 }
 
 // The prefill GEMM of one chunk (<= 64 rows of one expert) against the strips of one workgroup, all of k: the input's
@@ -1104,12 +1107,13 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
     load_words<BITS>(rec + 64 * BITS, dB);
     StageRegs r;
     stage_load(src, pitch, row0, nrows, scol, r, tid);
-    stage_store(bufp(0, sh), kp, nrows, r, tid);
+    stage_store(bufp(0, sh), kp, r, tid);
     __syncthreads();
     const Mul1Consts k = mul1_consts();
     const int rr = lane & 15, g = lane >> 4;
     for (int kb = 0; kb < nb; ++kb) {
-        if (kb + 1 < nb) stage_load(src, pitch, row0, nrows, scol + (kb + 1) * 128, r, tid);
+        // the next block, or at the last a harmless reload of it: unconditional, like the codes' refills
+        stage_load(src, pitch, row0, nrows, scol + min(kb + 1, nb - 1) * 128, r, tid);
         const uint16_t* Ab = bufp(kb & 1, sh);
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -1136,28 +1140,24 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
                 }
             }
         }
-        if (kb + 1 < nb) {
-            stage_store(bufp((kb + 1) & 1, sh), kp, nrows, r, tid);
-        }
+        if (kb + 1 < nb) stage_store(bufp((kb + 1) & 1, sh), kp, r, tid);
         __syncthreads();
     }
 }
 
 // gate_up's prefill GEMM with its epilogue: one workgroup of 8 waves per (chunk, h-block hb): waves 0..3 the 4 gate
 // strips of columns 128 hb .., waves 4..7 the 4 up strips of columns N / 2 + 128 hb .., each half of xr staged for
-// its waves. The raw sums go to part (a checker's view); then the accumulations cross LDS and each wave finishes whole
-// rows of the block: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh)))
-// (kernels/exl3ref/ref.c:187-212) into y at columns 128 hb... A negative sorted_tok, and a narrower class's blocks past
-// its width, are written zero; rows no run holds are k_zero_dead's.
+// its waves. With keep_sums the raw sums go to part (a checker's view). Then the accumulations cross LDS and each
+// wave finishes whole rows of the block: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step
+// f16(had(f16(h * dn_suh))) (kernels/exl3ref/ref.c:187-212) into y at columns 128 hb... A negative sorted_tok, and a
+// narrower class's blocks past its width, are written zero; rows no run holds are k_zero_dead's.
 template <int BITS, int CB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
     constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
     int hb, chunk;
-    xcd_unit(a.n_grp / 2, hb, chunk);
+    if (!xcd_unit(a.n_grp / 2, min(a.plan[0], a.max_chunks), hb, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nch = min(a.plan[0], a.max_chunks);
-    if (chunk >= nch) return;
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
     const Exl3c4Class& K = a.cls[class_of(a, e)];
@@ -1187,8 +1187,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         for (int q = 0; q < 4; ++q) {
             const int row = t * 16 + rg * 4 + q;
             if (row < nrows) {
-                a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
-                a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
+                if (a.keep_sums) {
+                    a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
+                    a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
+                }
                 acc_l[row * ACC_PITCH + col_l] = acc[t][0][q];
                 acc_l[row * ACC_PITCH + col_l + 8] = acc[t][1][q];
             }
@@ -1215,15 +1217,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
 // down's prefill GEMM: one workgroup per (chunk, 128-column output block); h (rotated, sorted-row order) in; the
 // epilogue (had128, x svh, bf16) in the workgroup through LDS, one row tile at a time. Writes every row of its chunk
-// in its block: a negative sorted_tok and a narrower class's tail as zero; raw sums to dacc.
+// in its block: a negative sorted_tok and a narrower class's tail as zero; with keep_sums the raw sums to dacc.
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
     int b, chunk;
-    xcd_unit(a.nblk, b, chunk);
+    if (!xcd_unit(a.nblk, min(a.plan[0], a.max_chunks), b, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int nch = min(a.plan[0], a.max_chunks);
-    if (chunk >= nch) return;
     const int4 ent = ((const int4*)(a.plan + 4))[chunk];
     const int e = ent.x, row0 = ent.y, nrows = ent.z;
     const Exl3c4Class& D = a.cls[class_of(a, e)];
@@ -1262,9 +1262,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             if (row < nrows) {
                 const int64_t r = row0 + row;
                 float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
-                float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
-                dacc[lane] = y0;
-                dacc[lane + 64] = y1;
+                if (a.keep_sums) {
+                    float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
+                    dacc[lane] = y0;
+                    dacc[lane + 64] = y1;
+                }
                 uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
                 if (a.sorted[r] < 0) {
                     out[lane] = 0;

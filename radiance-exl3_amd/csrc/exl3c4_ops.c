@@ -280,8 +280,9 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->blk_per_wave = 1;
 }
 
-/* The events of a timed launch go to exactly one kernel of the sequence. */
-typedef struct Timed { int kernel; void *ev0, *ev1; } Timed;
+/* How a launch runs: the events of a timed launch go to exactly one kernel of the sequence; keep_sums has the
+ * prefill GEMMs also write their f32 sums to scratch (exl3c4_launch_checked). */
+typedef struct Timed { int kernel; void *ev0, *ev1; int keep_sums; } Timed;
 #define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
 
 /* down's classes: its own, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
@@ -308,6 +309,7 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     int rc;
     Exl3c4Launch p;
     base_args(o, k, s, &p);
+    p.keep_sums = t->keep_sums;
     p.row_info = (int32_t*)(s + k->row_info);
     p.plan = (int32_t*)(s + k->plan);
     p.max_chunks = (int32_t)k->max_chunks;
@@ -399,12 +401,14 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
     }
 }
 
-/* The launches of each op on the stream -- no planning pass: every workgroup finds its rows' expert itself.
+/* The launches of each op on the stream. Decode (fewer than 64 and 8 n_expert sorted rows: prefill_path) has no
+ * planning pass: every workgroup finds its rows' expert itself.
  *   prep_gu       the input rotation
  *   gate_up       its GEMM (input rotation staged inside), then its epilogue
  *   down          its GEMM, whose workgroups stage (and rotate) their rows and finish their output blocks
  *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums; from
- *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1) */
+ *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1)
+ * Prefill (launch_prefill) plans 64-row chunks of one expert first and runs one GEMM kernel a projection. */
 static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t,
                        int32_t* ctr) {
     int rc;
@@ -463,7 +467,12 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
 }
 
 int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
-    const Timed t = { -1, NULL, NULL };
+    const Timed t = { -1, NULL, NULL, 0 };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
+}
+
+int exl3c4_launch_checked(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
+    const Timed t = { -1, NULL, NULL, 1 };
     return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
 }
 
@@ -487,7 +496,7 @@ int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, v
     carve(o, o->T, &k);
     if (k.gd1 && ctr && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
         return EXL3C4_E_SCRATCH;
-    const Timed t = { -1, NULL, NULL };
+    const Timed t = { -1, NULL, NULL, 0 };
     return launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL);
 }
 
@@ -499,7 +508,7 @@ int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes,
     Carve k;
     carve(o, o->T, &k);
     if (!runs_kernel(o, &k, kernel)) return EXL3C4_E_INVAL;
-    const Timed t = { kernel, ev_start, ev_stop };
+    const Timed t = { kernel, ev_start, ev_stop, 0 };
     return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
 }
 

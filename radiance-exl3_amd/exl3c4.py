@@ -55,6 +55,8 @@ def lib():
         L.exl3c4_scratch_bytes.argtypes = [C.POINTER(Op)]
         L.exl3c4_launch.restype = C.c_int
         L.exl3c4_launch.argtypes = [C.POINTER(Op), _p, _i64, _p]
+        L.exl3c4_launch_checked.restype = C.c_int
+        L.exl3c4_launch_checked.argtypes = [C.POINTER(Op), _p, _i64, _p]
         L.exl3c4_dequant.restype = C.c_int
         L.exl3c4_dequant.argtypes = [_p, _i32, _i32, _i32, _i32, _p, _i64, _p]
         L.exl3c4_record_bytes.restype = _i64
@@ -227,6 +229,12 @@ def launch(o: Op, scratch=None, stream=None) -> int:
     """Runs one op; returns the status (0 OK). `scratch`: a uint8 device tensor of >= scratch_bytes(o)."""
     n = 0 if scratch is None else scratch.numel()
     return int(lib().exl3c4_launch(C.byref(o), _ptr(scratch), n, _stream(stream)))
+
+
+def launch_checked(o: Op, scratch=None, stream=None) -> int:
+    """launch, and a prefill-path launch also leaves its GEMMs' f32 sums in `scratch` for partial_sums."""
+    n = 0 if scratch is None else scratch.numel()
+    return int(lib().exl3c4_launch_checked(C.byref(o), _ptr(scratch), n, _stream(stream)))
 
 
 def ctr_bytes(o: Op) -> int:

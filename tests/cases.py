@@ -231,18 +231,27 @@ class Dev:
                                           svh=d["svh"], dn_suh=d.get("dn_suh") if dn_suh else None))
         return out
 
-    def _run(self, o, expect=0):
+    def _run(self, o, y, *inputs, expect=0):
+        """Launches `o` (whose output is `y`); `inputs`: device tensors the op points to that the caller made for it,
+        kept alive with it so that last_acc can launch it again."""
         s = self.ex.alloc_scratch(o)
         rc = self.ex.launch(o, s)
         assert rc == expect, f"launch status {self.ex.STATUS.get(rc, rc)}"
         self.torch.cuda.synchronize()
-        self.last = (o, s)
+        self.last = (o, y, inputs)
         self.status = self.ex.launch_status(o, s) if rc == 0 else None
         assert self.status in (None, 0), f"gate_up_down's single kernel left status {self.status}"
 
     def last_acc(self, gemm=0):
-        """The f32 accumulations the last launch left in its scratch."""
-        o, s = self.last
+        """The f32 accumulations of the last launch: the same op again through exl3c4_launch_checked (which also
+        leaves the prefill GEMMs' sums in scratch), whose output must be the production launch's, bit for bit."""
+        o, y, _ = self.last
+        before = y.clone()
+        s = self.ex.alloc_scratch(o)
+        rc = self.ex.launch_checked(o, s)
+        assert rc == 0, f"launch_checked status {self.ex.STATUS.get(rc, rc)}"
+        self.torch.cuda.synchronize()
+        assert self.torch.equal(y, before), "exl3c4_launch_checked wrote another output than exl3c4_launch"
         return self.ex.partial_sums(o, s, gemm)
 
     def out(self, cols, fill=0x7E7E):
@@ -254,7 +263,7 @@ class Dev:
         y = self.out(2 * C, fill=np.int16(np.uint16(prefill).view(np.int16)))
         o = self.ex.make_op(self.ex.PREP_GU, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
                             c.n_tok, c.top_k, x_bf16=c.x_bf16)
-        self._run(o)
+        self._run(o, y)
         return y.cpu().numpy().view(np.uint16)
 
     def gate_up(self, h_rot=0, a_rot=0, xr=None):
@@ -264,7 +273,7 @@ class Dev:
         x = xr if a_rot else self.x
         o = self.ex.make_op(self.ex.GATE_UP, c.bits, c.cb, self.cls("gu"), x, self.sorted_tok, self.off, y,
                             c.n_tok, c.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=c.x_bf16 and not a_rot)
-        self._run(o)
+        self._run(o, y, x)
         return y.cpu().numpy().view(np.uint16)
 
     def down(self, h, h_rot=0):
@@ -274,7 +283,7 @@ class Dev:
         hd = self.torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).to("cuda")
         o = self.ex.make_op(self.ex.DOWN, c.bits, c.cb, self.cls("dn"), hd, self.sorted_tok, self.off, y,
                             c.n_tok, c.top_k, h_rot=h_rot)
-        self._run(o)
+        self._run(o, y, hd)
         return y.cpu().numpy().view(np.uint16)
 
     def gate_up_down(self):
@@ -285,5 +294,5 @@ class Dev:
         dn = [self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in self.tabs["dn"]]
         o = self.ex.make_op(self.ex.GU_DN, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
                             c.n_tok, c.top_k, dn=dn, x_bf16=c.x_bf16)
-        self._run(o)
+        self._run(o, y)
         return y.cpu().numpy().view(np.uint16)
