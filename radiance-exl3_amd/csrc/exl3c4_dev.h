@@ -23,6 +23,14 @@ extern "C" {
 #define EXL3C4_SYNC_DONE 32
 /* Rows of one chunk on the prefill path (four MFMA row tiles decode-shared). */
 #define EXL3C4_PF_ROWS 64
+/* The prefill plan: PF_PLAN_HDR int32s, then int4 {expert, row0, rows, 0} per chunk. Header: [0] the chunk count;
+ * [PF_XCD_GU + x], [PF_XCD_DN + x] (x = 0 .. 8): the first chunk of XCD x for gate_up's and down's GEMM ([.. + 8] = the
+ * count). A chunk of t 16-row tiles costs about PF_W_GU + t (gate_up) and PF_W_DN + t (down) units of workgroup time. */
+#define EXL3C4_PF_PLAN_HDR 32
+#define EXL3C4_PF_XCD_GU 8
+#define EXL3C4_PF_XCD_DN 20
+#define EXL3C4_PF_W_GU 10
+#define EXL3C4_PF_W_DN 3
 
 typedef struct Exl3c4Launch {
     Exl3c4Class    cls[4];        /* the GEMM's weight classes (gate_up's, or down's); prep: the scale source */

@@ -229,15 +229,32 @@ __device__ __forceinline__ void decode_seg_impl(const uint32_t (&v)[BITS + 1], u
     (decode_pair<BITS, CB, 2 * P>(v, B, k), ...);
 }
 
+// A lane's segment as its decode window (decode_pair's v): the K words reversed, then the previous segment of the same
+// tile's last word -- two lanes down, circularly within the 16-lane row (c = 2 s + t).
+template <int BITS>
+__device__ __forceinline__ void segment_window(const uint32_t (&d)[BITS], uint32_t (&v)[BITS + 1]) {
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) v[w] = d[BITS - 1 - w];
+    v[BITS] = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[BITS - 1], 0x122, 0xF, 0xF, false);
+}
+
 // One lane's segment -> its 32 weights as the four B operands (B[0..3] B_a, [4..7] B_b, [8..11] B_c, [12..15] B_d).
 template <int BITS, int CB>
 __device__ __forceinline__ void decode_segment(const uint32_t (&d)[BITS], uint32_t (&B)[16], const Mul1Consts& k) {
     uint32_t v[BITS + 1];
-#pragma unroll
-    for (int w = 0; w < BITS; ++w) v[w] = d[BITS - 1 - w];
-    // the previous segment of the same tile: two lanes down, circularly within the 16-lane row (c = 2 s + t)
-    v[BITS] = (uint32_t)__builtin_amdgcn_mov_dpp((int)d[BITS - 1], 0x122, 0xF, 0xF, false);
+    segment_window<BITS>(d, v);
     decode_seg_impl<BITS, CB>(v, B, k, std::make_integer_sequence<int, 16>{});
+}
+
+// Quarter QT of a segment's decode: positions 8 QT .. 8 QT + 7 (four pairs).
+template <int BITS, int CB, int QT, int... P>
+__device__ __forceinline__ void decode_quarter_impl(const uint32_t (&v)[BITS + 1], uint32_t (&B)[16],
+                                                    const Mul1Consts& k, std::integer_sequence<int, P...>) {
+    (decode_pair<BITS, CB, 8 * QT + 2 * P>(v, B, k), ...);
+}
+template <int BITS, int CB, int QT>
+__device__ __forceinline__ void decode_quarter(const uint32_t (&v)[BITS + 1], uint32_t (&B)[16], const Mul1Consts& k) {
+    decode_quarter_impl<BITS, CB, QT>(v, B, k, std::make_integer_sequence<int, 4>{});
 }
 
 // A lane's K words of one block: K u32 at p (4-byte aligned).
@@ -861,14 +878,19 @@ __global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
 // writes it, or down's rotated h), the GEMMs, and the epilogues.
 
 // One workgroup: every expert's run clamped to [0, T) cut into chunks of at most 64 rows, in expert order
-// (kernels/exl3r4d/launch.c:14-15 clamps the runs).
+// (kernels/exl3r4d/launch.c:14-15 clamps the runs); then, for each GEMM, the chunks dealt to the 8 XCDs in contiguous
+// ranges of about equal cost (a chunk of t tiles: W + t; its midpoint in cost order picks the XCD).
+__device__ __forceinline__ int pf_xcd_of(int p_excl, int cost, int total) {
+    return min(7, (int)((8ll * (2ll * p_excl + cost)) / (2ll * max(total, 1))));
+}
 __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
     __shared__ int scan[1024];
-    __shared__ int carry_s;
+    __shared__ int carry_s, tiles_s, cnt_g[8], cnt_d[8];
     const int tid = threadIdx.x;
-    if (tid == 0) carry_s = 0;
+    if (tid == 0) carry_s = tiles_s = 0;
+    if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
     __syncthreads();
-    int4* ent = (int4*)(a.plan + 4);
+    int4* ent = (int4*)(a.plan + EXL3C4_PF_PLAN_HDR);
     for (int base = 0; base < a.n_expert; base += 1024) {
         const int e = base + tid;
         int lo = 0, hi = 0, n = 0;
@@ -886,25 +908,82 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
             __syncthreads();
         }
         const int first = carry_s + scan[tid] - n;
+        int tiles = 0;
         for (int q = 0; q < n; ++q) {
             const int at = first + q;
             if (at < a.max_chunks) {
-                const int r0 = lo + q * EXL3C4_PF_ROWS;
-                ent[at] = make_int4(e, r0, min(EXL3C4_PF_ROWS, hi - r0), 0);
+                const int r0 = lo + q * EXL3C4_PF_ROWS, rows = min(EXL3C4_PF_ROWS, hi - r0);
+                ent[at] = make_int4(e, r0, rows, 0);
+                tiles += (rows + 15) >> 4;
             }
         }
+        if (tiles) atomicAdd(&tiles_s, tiles);
         __syncthreads();
         if (tid == 1023) carry_s += scan[1023];
         __syncthreads();
     }
-    if (tid == 0) a.plan[0] = min(carry_s, a.max_chunks);
+    const int nch = min(carry_s, a.max_chunks);
+    const int tot_g = EXL3C4_PF_W_GU * nch + tiles_s, tot_d = EXL3C4_PF_W_DN * nch + tiles_s;
+    // the chunks' tile prefix (this workgroup wrote the entries: visible after the barrier above)
+    int carry = 0;
+    for (int base = 0; base < nch; base += 1024) {
+        const int c = base + tid;
+        const int t = c < nch ? (ent[c].z + 15) >> 4 : 0;
+        scan[tid] = t;
+        __syncthreads();
+        for (int d = 1; d < 1024; d <<= 1) {
+            const int u = tid >= d ? scan[tid - d] : 0;
+            __syncthreads();
+            scan[tid] += u;
+            __syncthreads();
+        }
+        if (c < nch) {
+            const int p = carry + scan[tid] - t;                  // tiles of the chunks before c
+            atomicAdd(&cnt_g[pf_xcd_of(EXL3C4_PF_W_GU * c + p, EXL3C4_PF_W_GU + t, tot_g)], 1);
+            atomicAdd(&cnt_d[pf_xcd_of(EXL3C4_PF_W_DN * c + p, EXL3C4_PF_W_DN + t, tot_d)], 1);
+        }
+        carry += scan[1023];
+        __syncthreads();
+    }
+    __syncthreads();
+    if (tid == 0) {
+        a.plan[0] = nch;
+        int bg = 0, bd = 0;
+        for (int x = 0; x < 8; ++x) {
+            a.plan[EXL3C4_PF_XCD_GU + x] = bg;
+            a.plan[EXL3C4_PF_XCD_DN + x] = bd;
+            bg += cnt_g[x];
+            bd += cnt_d[x];
+        }
+        a.plan[EXL3C4_PF_XCD_GU + 8] = bg;
+        a.plan[EXL3C4_PF_XCD_DN + 8] = bd;
+    }
 }
 
-// had128 over 128-blocks held 8 consecutive elements a lane (lane l of a 16-lane row: elements 8 (l % 16) .. + 7 of
-// its block): the stages h = 1, 2, 4 inside the lane, h = 8, 16, 32, 64 across lanes l ^ 1, ^ 2, ^ 4, ^ 8 (within the
-// row) as in had128_wave -- v_fmac by +-1 with a DPP partner, negated results where the lane bit is set, undone by
-// the sign of the final scale. The same roundings as the reference's stages, so the same bits.
-__device__ __forceinline__ void had128_x8(float (&v)[8], int lane) {
+// had128 over 128-blocks held 8 consecutive elements a lane: lane l of a 16-lane row holds the elements 8 g .. 8 g + 7
+// of its block, g = rot_group(l) = l ^ 3 where bit 2 of l is set, else l. The stages h = 1, 2, 4 run inside the lane;
+// h = 8, 16, 32, 64 (bits 0 .. 3 of g) pair lane l with l ^ 1, l ^ 2, l ^ 7, l ^ 8 -- the lanes whose g differs in that
+// bit alone, each one DPP move (quad_perm, quad_perm, row_half_mirror, row_ror 8) -- as in had128_wave: v_fmac by
+// c = -1 on the lanes whose g has the stage's bit set leaves them the NEGATED result, the partner (same lower bits of
+// g) carries the same sign, and the final multiply by -1/sqrt(128) where popcount(g) is odd undoes it. The reference's
+// stages in its order with its roundings (common/exl3_decode.c:172-189), so the same bits.
+__device__ __forceinline__ int rot_group(int l) { return l ^ (((l >> 2) & 1) * 3); }
+#define HAD_DPP8_OP(I, CTRL) "v_fmac_f32_dpp %" #I ", %" #I ", %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"
+// one stage over the 8 values: a lane's v[j] was written 8 moves before it is read, so one s_nop (the DPP read-after-
+// VALU-write distance) opens the block and none sits between its moves
+#define HAD_DPP8(v, c, CTRL)                                                                                   \
+    asm volatile("s_nop 1\n\t" HAD_DPP8_OP(0, CTRL) HAD_DPP8_OP(1, CTRL) HAD_DPP8_OP(2, CTRL)               \
+                 HAD_DPP8_OP(3, CTRL) HAD_DPP8_OP(4, CTRL) HAD_DPP8_OP(5, CTRL) HAD_DPP8_OP(6, CTRL)           \
+                 HAD_DPP8_OP(7, CTRL)                                                                         \
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),       \
+                   "+v"(v[7])                                                                                 \
+                 : "v"(c))
+struct RotSigns { float c1, c2, c4, c8, sc; };
+__device__ __forceinline__ RotSigns rot_signs(int g) {
+    return RotSigns{ (g & 1) ? -1.f : 1.f, (g & 2) ? -1.f : 1.f, (g & 4) ? -1.f : 1.f, (g & 8) ? -1.f : 1.f,
+                     (__builtin_popcount(g) & 1) ? -kHadScale : kHadScale };
+}
+__device__ __forceinline__ void had128_x8(float (&v)[8], const RotSigns& k) {
 #pragma unroll
     for (int h = 1; h < 8; h <<= 1)
 #pragma unroll
@@ -914,41 +993,32 @@ __device__ __forceinline__ void had128_x8(float (&v)[8], int lane) {
                 v[j] = a + b;
                 v[j + h] = a - b;
             }
-    const float c1 = (lane & 1) ? -1.f : 1.f, c2 = (lane & 2) ? -1.f : 1.f, c4 = (lane & 4) ? -1.f : 1.f;
-    const float c8 = (lane & 8) ? -1.f : 1.f;
+    HAD_DPP8(v, k.c1, "quad_perm:[1,0,3,2]");
+    HAD_DPP8(v, k.c2, "quad_perm:[2,3,0,1]");
+    HAD_DPP8(v, k.c4, "row_half_mirror");
+    HAD_DPP8(v, k.c8, "row_ror:8");
 #pragma unroll
-    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c1, "quad_perm:[1,0,3,2]");
-#pragma unroll
-    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c2, "quad_perm:[2,3,0,1]");
-    const bool hi4 = lane & 4;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = fmaf(partner4(v[j], hi4), c4, v[j]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) HAD_DPP(v[j], c8, "row_ror:8");
-    const float sc = (__builtin_popcount(lane & 15) & 1) ? -kHadScale : kHadScale;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = v[j] * sc;
+    for (int j = 0; j < 8; ++j) v[j] = v[j] * k.sc;
 }
 
-// 8 consecutive halves at p (16-byte aligned: one load; else eight)
-__device__ __forceinline__ void load8h(const uint16_t* p, bool wide, uint16_t (&h)[8]) {
+// 8 consecutive halves at p as 4 dwords (16-byte aligned: one load; else eight)
+__device__ __forceinline__ void load8w(const uint16_t* p, bool wide, uint32_t (&w)[4]) {
     if (wide) {
         const uint4 q = *(const uint4*)p;
-        const uint32_t w[4] = { q.x, q.y, q.z, q.w };
-#pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+        w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) h[j] = ldg16(p, j);
+        for (int j = 0; j < 4; ++j) w[j] = (uint32_t)ldg16(p, 2 * j) | ((uint32_t)ldg16(p, 2 * j + 1) << 16);
     }
 }
 
 // The rotation into scratch, one wave per sorted row, 8 consecutive elements a lane: a pass covers 4 128-blocks of
 // each half (one 16-byte load of x, one of each scale and one store a half a lane), and the loads of up to ROT_PASSES
 // passes go out together: gate_up's xr (halves 0 and 1 from the same token row: suh, suh1 of the row's expert) or
-// down's rotated h (one half: down's suh, sorted rows in). The rows are dealt to the XCDs in contiguous ranges, so a
-// run's rows (one expert's scales) share an L2. Rows no run holds are not written (nothing reads them); a negative
-// sorted_tok gives zeros.
+// down's rotated h (one half: down's suh, sorted rows in). The first step f16(x su) is one f16 multiply (v_pk_mul_f16:
+// the exact product rounded once, as f16(f32(x) f32(su)) rounds it; bf16 x: in f32, then rounded). The rows are dealt
+// to the XCDs in contiguous ranges, so a run's rows (one expert's scales) share an L2. Rows no run holds are not
+// written (nothing reads them); a negative sorted_tok gives zeros.
 constexpr int ROT_PASSES = 2;
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63;
@@ -965,13 +1035,15 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int C = K.cols;
     uint16_t* out = (uint16_t*)a.y + (int64_t)i * a.y_pitch;
     const int npass = (C / 128 + 3) / 4;
+    const int g = rot_group(lane & 15), lcol = 128 * (lane >> 4) + 8 * g;   // the lane's columns in a pass
     if (tok < 0) {
         for (int p = 0; p < npass * halves; ++p) {
-            const int col = (p % npass) * 512 + 8 * lane;
+            const int col = (p % npass) * 512 + lcol;
             if (col < C) *(uint4*)(out + (p / npass) * C + col) = uint4{ 0, 0, 0, 0 };
         }
         return;
     }
+    const RotSigns ks = rot_signs(g);
     int64_t src = halves == 2 ? tok / a.top_k : i;
     src = src < a.x_rows ? src : a.x_rows - 1;
     const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch;
@@ -981,14 +1053,14 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const bool sw = (((uintptr_t)s0 | (uintptr_t)s1) & 15) == 0;
     const bool bf = halves == 2 && a.x_dtype == EXL3C4_BF16;
     for (int p0 = 0; p0 < npass; p0 += ROT_PASSES) {
-        uint16_t xh[ROT_PASSES][8], sh[2][ROT_PASSES][8];
+        uint32_t xq[ROT_PASSES][4], sq[2][ROT_PASSES][4];
 #pragma unroll
         for (int q = 0; q < ROT_PASSES; ++q) {
-            int col = (p0 + q) * 512 + 8 * lane;
-            col = col < C ? col : 8 * (lane & 15);                   // past the row: reload the first block (unused)
-            load8h(x + col, xw, xh[q]);
-            load8h(s0 + col, sw, sh[0][q]);
-            if (halves == 2) load8h(s1 + col, sw, sh[1][q]);
+            int col = (p0 + q) * 512 + lcol;
+            col = col < C ? col : 8 * g;                            // past the row: reload the first block (unused)
+            load8w(x + col, xw, xq[q]);
+            load8w(s0 + col, sw, sq[0][q]);
+            if (halves == 2) load8w(s1 + col, sw, sq[1][q]);
         }
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
@@ -998,12 +1070,26 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
                 if (p0 + q >= npass) break;
                 float v[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = h2f(f2h((bf ? bf2f(xh[q][j]) : h2f(xh[q][j])) * h2f(sh[m][q][j])));
-                had128_x8(v, lane);
+                for (int j = 0; j < 4; ++j) {
+                    if (bf) {
+                        const uint32_t xb = xq[q][j], sb = sq[m][q][j];
+                        v[2 * j] = h2f(f2h(bf2f((uint16_t)xb) * h2f((uint16_t)sb)));
+                        v[2 * j + 1] = h2f(f2h(bf2f((uint16_t)(xb >> 16)) * h2f((uint16_t)(sb >> 16))));
+                    } else {
+                        const half2_t pr = __builtin_bit_cast(half2_t, xq[q][j]) * __builtin_bit_cast(half2_t, sq[m][q][j]);
+                        v[2 * j] = (float)pr.x;
+                        v[2 * j + 1] = (float)pr.y;
+                    }
+                }
+                had128_x8(v, ks);
                 uint32_t o[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) o[j] = (uint32_t)f2h(v[2 * j]) | ((uint32_t)f2h(v[2 * j + 1]) << 16);
-                const int col = (p0 + q) * 512 + 8 * lane;
+                for (int j = 0; j < 4; ++j) {
+                    typedef float float2v __attribute__((ext_vector_type(2)));
+                    const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
+                    o[j] = __builtin_bit_cast(uint32_t, hv);
+                }
+                const int col = (p0 + q) * 512 + lcol;
                 if (col < C) *(uint4*)(out + m * C + col) = uint4{ o[0], o[1], o[2], o[3] };
             }
         }
@@ -1071,27 +1157,73 @@ __device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs
 }
 
 // The prefill GEMMs' workgroups and XCDs: XCD x (the dispatcher deals linear ids g to the XCDs in turn, x = g % 8)
-// takes the contiguous chunks [x nq, x nq + nq) of the plan, nq = ceil(chunks / 8), its slot g / 8 = per q + u running
-// unit u (0 .. per-1: the chunk's column groups or blocks) of its q-th chunk. A chunk's units run side by side in one
-// L2, so its staged rows come from HBM once; and the plan lists an expert's chunks one after another, so they too
-// share an L2 and, running close in time, read the expert's codes from HBM about once. Every chunk costs about the
-// same (its decode), so equal ranges balance the XCDs. False for a workgroup with no chunk (the grid covers the
-// plan's bound). (Where a workgroup lands changes no bits.)
-__device__ __forceinline__ bool xcd_unit(int per, int nch, int& unit, int& chunk) {
+// takes the plan's contiguous chunk range [xb[x], xb[x + 1]) -- ranges of about equal cost, from k_plan -- its slot
+// g / 8 = per q + u running unit u (0 .. per-1: the chunk's column groups or blocks) of its q-th chunk. A chunk's units
+// run side by side in one L2, so its staged rows come from HBM once; and the plan lists an expert's chunks one after
+// another, so they too share an L2 and, running close in time, read the expert's codes from HBM about once. False
+// for a workgroup with no chunk (the grid covers pf_xcd_bound chunks an XCD). (Where a workgroup lands changes no
+// bits.)
+__device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, int& unit, int& chunk) {
     const int g = (int)blockIdx.x, slot = g >> 3, x = g & 7;
-    const int nq = (nch + 7) >> 3, q = slot / per;
+    const int q = slot / per;
     unit = slot - q * per;
-    chunk = x * nq + q;
-    return q < nq && chunk < nch;
+    chunk = xb[x] + q;
+    return chunk < xb[x + 1];
+}
+
+// One k-step of the prefill GEMM, software-pipelined by a step: the MFMAs of step ks (B operands Bc, decoded a step
+// earlier) tile by tile, each tile's four followed by a quarter of step ks + 1's decode (code dn) into Bn. The wave
+// issues that decode while the matrix core runs the MFMAs; the next tile's A comes from LDS meanwhile. Every register
+// an MFMA reads stays live (an empty asm use) until the decode quarter after it has issued -- 30-odd VALU
+// instructions, well past the cycles in which the MFMA reads its A and B -- so nothing the compiler places there can
+// overwrite an operand still being read (gfx950 does not interlock a VALU write against an in-flight 16x16x32 MFMA's
+// A/B reads, and the compiler does not pad for it).
+template <int BITS, int CB, int NT, int T>
+__device__ __forceinline__ void pf_tile(const uint16_t* Ab, int kp, const half8_t (&bq)[4], half8_t& Aa,
+                                        half8_t& Ac, const uint32_t (&v)[BITS + 1], uint32_t (&Bn)[16],
+                                        const Mul1Consts& k, float4_t (&acc)[4][2]) {
+    if constexpr (T < NT) {
+        acc[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, bq[0], acc[T][0], 0, 0, 0);
+        acc[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, bq[1], acc[T][1], 0, 0, 0);
+        acc[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, bq[2], acc[T][0], 0, 0, 0);
+        acc[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, bq[3], acc[T][1], 0, 0, 0);
+    }
+    half8_t Na, Nc;
+    if constexpr (T + 1 < NT) {                                   // the next tile's A
+        const uint16_t* arow = Ab + 16 * kp;
+        Na = *(const half8_t*)arow;
+        Nc = *(const half8_t*)(arow + 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    decode_quarter<BITS, CB, T>(v, Bn, k);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (T < NT) asm volatile("" ::"v"(Aa), "v"(Ac));
+    if constexpr (T + 1 < NT) { Aa = Na; Ac = Nc; }
+}
+template <int BITS, int CB, int NT>
+__device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&Bc)[16],
+                                        const uint32_t (&dn)[BITS], uint32_t (&Bn)[16], const Mul1Consts& k,
+                                        float4_t (&acc)[4][2]) {
+    uint32_t v[BITS + 1];
+    segment_window<BITS>(dn, v);
+    const half8_t bq[4] = { as_half8(Bc[0], Bc[1], Bc[2], Bc[3]), as_half8(Bc[8], Bc[9], Bc[10], Bc[11]),
+                            as_half8(Bc[4], Bc[5], Bc[6], Bc[7]), as_half8(Bc[12], Bc[13], Bc[14], Bc[15]) };
+    half8_t Aa = *(const half8_t*)Ab, Ac = *(const half8_t*)(Ab + 8);
+    pf_tile<BITS, CB, NT, 0>(Ab, kp, bq, Aa, Ac, v, Bn, k, acc);
+    pf_tile<BITS, CB, NT, 1>(Ab + 16 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
+    pf_tile<BITS, CB, NT, 2>(Ab + 32 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
+    pf_tile<BITS, CB, NT, 3>(Ab + 48 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
+    asm volatile("" ::"v"(bq[0]), "v"(bq[1]), "v"(bq[2]), "v"(bq[3]));
 }
 
 // The prefill GEMM of one chunk (<= 64 rows of one expert) against the strips of one workgroup, all of k: the input's
 // 128-k blocks stream through two LDS buffers a half; each wave decodes its strip's step once and runs it against every
-// row tile. NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8 waves, two staged inputs (columns k
-// and half_off + k), thread t staging half t / 256 and wave w reading half w / 4. Accumulations: acc[row tile][strip
-// half].
-template <int BITS, int CB, int NH>
-__device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
+// row tile, a step behind its decode (pf_step). NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8
+// waves, two staged inputs (columns k and half_off + k), thread t staging half t / 256 and wave w reading half w / 4.
+// NT: the chunk's 16-row tiles (ceil(nrows / 16)), a template argument so that the loop holds no branch on it.
+// Accumulations: acc[row tile][strip half].
+template <int BITS, int CB, int NH, int NT>
+__device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
                                         int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
     const int lane = threadIdx.x & 63;
@@ -1100,48 +1232,44 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
     const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
     const int scol = col_off + sh * half_off;                     // this thread's staged input column
     auto bufp = [&](int b, int h) { return lds + (b * NH + h) * 64 * kp; };
-    const int ntile = (nrows + 15) >> 4;
     const gu32p rec = (gu32p)tab_entry(W.codes, W.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    // the codes of the steps ahead: dA even steps, dB odd; each refill 3 steps ahead of the step it serves (clamped:
+    // past the stream a harmless reload of the last step, unconditional so that the waits count exactly)
     uint32_t dA[BITS], dB[BITS];
     load_words<BITS>(rec, dA);
     load_words<BITS>(rec + 64 * BITS, dB);
     StageRegs r;
     stage_load(src, pitch, row0, nrows, scol, r, tid);
+    const Mul1Consts k = mul1_consts();
+    uint32_t B0[16], B1[16];                                      // the decoded steps: even in B0, odd in B1
+    decode_segment<BITS, CB>(dA, B0, k);
+    load_words<BITS>(rec + (int64_t)min(2, ksteps - 1) * 64 * BITS, dA);
     stage_store(bufp(0, sh), kp, r, tid);
     __syncthreads();
-    const Mul1Consts k = mul1_consts();
     const int rr = lane & 15, g = lane >> 4;
     for (int kb = 0; kb < nb; ++kb) {
         // the next block, or at the last a harmless reload of it: unconditional, like the codes' refills
         stage_load(src, pitch, row0, nrows, scol + min(kb + 1, nb - 1) * 128, r, tid);
-        const uint16_t* Ab = bufp(kb & 1, sh);
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int ks = 2 * kb + s;
-            uint32_t B[16];
-            decode_segment<BITS, CB>(s ? dB : dA, B, k);
-            // the step two ahead, or past the stream a harmless reload of the last: unconditional, so the waits for
-            // the codes are counted, not drained
-            const int nx = ks + 2 < ksteps ? ks + 2 : ksteps - 1;
-            if (s == 0) load_words<BITS>(rec + nx * 64 * BITS, dA);
-            else load_words<BITS>(rec + nx * 64 * BITS, dB);
-            const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
-            const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                if (t < ntile) {
-                    const uint16_t* arow = Ab + (t * 16 + rr) * kp + s * EXL3C4_KSTEP + 16 * g;
-                    const half8_t Aa = *(const half8_t*)arow, Ac = *(const half8_t*)(arow + 8);
-                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b0, acc[t][0], 0, 0, 0);
-                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b1, acc[t][1], 0, 0, 0);
-                    acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b2, acc[t][0], 0, 0, 0);
-                    acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b3, acc[t][1], 0, 0, 0);
-                    mfma_guard(Aa, Ac, b0, b1, b2, b3);
-                }
-            }
-        }
+        const uint16_t* Ab = bufp(kb & 1, sh) + rr * kp + 16 * g;
+        const int ks = 2 * kb;
+        pf_step<BITS, CB, NT>(Ab, kp, B0, dB, B1, k, acc);       // step ks; decodes ks + 1
+        load_words<BITS>(rec + (int64_t)min(ks + 3, ksteps - 1) * 64 * BITS, dB);
+        pf_step<BITS, CB, NT>(Ab + EXL3C4_KSTEP, kp, B1, dA, B0, k, acc);   // step ks + 1; decodes ks + 2
+        load_words<BITS>(rec + (int64_t)min(ks + 4, ksteps - 1) * 64 * BITS, dA);
         if (kb + 1 < nb) stage_store(bufp((kb + 1) & 1, sh), kp, r, tid);
         __syncthreads();
+    }
+}
+
+template <int BITS, int CB, int NH>
+__device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
+                                        const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
+                                        int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
+    switch ((nrows + 15) >> 4) {
+    case 1: pf_gemm_nt<BITS, CB, NH, 1>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
+    case 2: pf_gemm_nt<BITS, CB, NH, 2>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
+    case 3: pf_gemm_nt<BITS, CB, NH, 3>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
+    default: pf_gemm_nt<BITS, CB, NH, 4>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
     }
 }
 
@@ -1156,10 +1284,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
     constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
     int hb, chunk;
-    if (!xcd_unit(a.n_grp / 2, min(a.plan[0], a.max_chunks), hb, chunk)) return;
+    if (!xcd_unit(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, hb, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
-    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
+    const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
+              nrows = __builtin_amdgcn_readfirstlane(ent.z);      // one chunk a workgroup: uniform
     const Exl3c4Class& K = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
     const int N = K.rows, KC = K.cols, width = N / 2;
@@ -1222,10 +1351,11 @@ template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
     int b, chunk;
-    if (!xcd_unit(a.nblk, min(a.plan[0], a.max_chunks), b, chunk)) return;
+    if (!xcd_unit(a.nblk, a.plan + EXL3C4_PF_XCD_DN, b, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int4 ent = ((const int4*)(a.plan + 4))[chunk];
-    const int e = ent.x, row0 = ent.y, nrows = ent.z;
+    const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
+    const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
+              nrows = __builtin_amdgcn_readfirstlane(ent.z);      // one chunk a workgroup: uniform
     const Exl3c4Class& D = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
     const int N = D.rows;
@@ -1460,11 +1590,15 @@ extern "C" int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* e
     return go(k_zero_dead, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
+// The most chunks k_plan can deal one XCD: the midpoints of its chunks lie in a stretch of total / 8 (total <=
+// (W + 4) chunks) and are at least W + 1 apart.
+static int pf_xcd_bound(int max_chunks, int w) { return (int)(((int64_t)(w + 4) * max_chunks) / (8 * (w + 1))) + 2; }
+
 extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->n_grp < 2 || a->max_chunks <= 0) return 0;
-    const dim3 grid((unsigned)(8 * (a->n_grp / 2) * ((a->max_chunks + 7) / 8)));
+    const dim3 grid((unsigned)(8 * (a->n_grp / 2) * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_GU)));
     if (ev0 && ev1)
         hipExtLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, *a);
     else
@@ -1476,7 +1610,8 @@ extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     const GemmFn f = by_bits<DnPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3((unsigned)(8 * a->nblk * ((a->max_chunks + 7) / 8))), (hipStream_t)stream, ev0, ev1, 0u, *a);
+    return go2(f, dim3((unsigned)(8 * a->nblk * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_DN))), (hipStream_t)stream, ev0, ev1,
+               0u, *a);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,
