@@ -65,6 +65,8 @@ typedef struct Exl3c4Launch {
     uint16_t*      hbuf;          /* gate_up_down in one launch: h (rotated, f16) of every chunk's rows [T][hbuf_pitch] */
     int64_t        hbuf_pitch;
     int32_t        keep_sums;     /* prefill: also leave the GEMMs' f32 sums in part / dacc (a checker's view) */
+    int32_t        tail_from;     /* prefill GEMMs: nonzero asks for workgroups that zero the rows no run holds after
+                                     the GEMM's (the launcher sets where they start) */
 } Exl3c4Launch;
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the
@@ -78,9 +80,7 @@ int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream);
 /* the prefill path */
 int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
-int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
-int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 /* the routing (exl3c4_route.hip) */

@@ -879,19 +879,20 @@ __global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
 
 // One workgroup: every expert's run clamped to [0, T) cut into chunks of at most 64 rows, in expert order
 // (kernels/exl3r4d/launch.c:14-15 clamps the runs); then, for each GEMM, the chunks dealt to the 8 XCDs in contiguous
-// ranges of about equal cost (a chunk of t tiles: W + t; its midpoint in cost order picks the XCD).
+// ranges of about equal cost (a chunk of t tiles: W + t; its midpoint in cost order picks the XCD); then each row's
+// owner. Its own kernel (k_plan), or the first workgroup of k_rot's launch, running beside the rotation.
 __device__ __forceinline__ int pf_xcd_of(int p_excl, int cost, int total) {
     return min(7, (int)((8ll * (2ll * p_excl + cost)) / (2ll * max(total, 1))));
 }
-__global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
-    __shared__ int scan[1024];
+template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& a) {
+    __shared__ int scan[NT];
     __shared__ int carry_s, tiles_s, cnt_g[8], cnt_d[8];
     const int tid = threadIdx.x;
     if (tid == 0) carry_s = tiles_s = 0;
     if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
     __syncthreads();
     int4* ent = (int4*)(a.plan + EXL3C4_PF_PLAN_HDR);
-    for (int base = 0; base < a.n_expert; base += 1024) {
+    for (int base = 0; base < a.n_expert; base += NT) {
         const int e = base + tid;
         int lo = 0, hi = 0, n = 0;
         if (e < a.n_expert) {
@@ -901,7 +902,7 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
         }
         scan[tid] = n;
         __syncthreads();
-        for (int d = 1; d < 1024; d <<= 1) {                     // inclusive scan
+        for (int d = 1; d < NT; d <<= 1) {                     // inclusive scan
             const int t = tid >= d ? scan[tid - d] : 0;
             __syncthreads();
             scan[tid] += t;
@@ -919,19 +920,19 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
         }
         if (tiles) atomicAdd(&tiles_s, tiles);
         __syncthreads();
-        if (tid == 1023) carry_s += scan[1023];
+        if (tid == NT - 1) carry_s += scan[NT - 1];
         __syncthreads();
     }
     const int nch = min(carry_s, a.max_chunks);
     const int tot_g = EXL3C4_PF_W_GU * nch + tiles_s, tot_d = EXL3C4_PF_W_DN * nch + tiles_s;
     // the chunks' tile prefix (this workgroup wrote the entries: visible after the barrier above)
     int carry = 0;
-    for (int base = 0; base < nch; base += 1024) {
+    for (int base = 0; base < nch; base += NT) {
         const int c = base + tid;
         const int t = c < nch ? (ent[c].z + 15) >> 4 : 0;
         scan[tid] = t;
         __syncthreads();
-        for (int d = 1; d < 1024; d <<= 1) {
+        for (int d = 1; d < NT; d <<= 1) {
             const int u = tid >= d ? scan[tid - d] : 0;
             __syncthreads();
             scan[tid] += u;
@@ -942,7 +943,7 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
             atomicAdd(&cnt_g[pf_xcd_of(EXL3C4_PF_W_GU * c + p, EXL3C4_PF_W_GU + t, tot_g)], 1);
             atomicAdd(&cnt_d[pf_xcd_of(EXL3C4_PF_W_DN * c + p, EXL3C4_PF_W_DN + t, tot_d)], 1);
         }
-        carry += scan[1023];
+        carry += scan[NT - 1];
         __syncthreads();
     }
     __syncthreads();
@@ -958,7 +959,19 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) {
         a.plan[EXL3C4_PF_XCD_GU + 8] = bg;
         a.plan[EXL3C4_PF_XCD_DN + 8] = bd;
     }
+    // each row's owner (row_info[i] = {e or -1, 0}): every row -1 first, then a chunk's rows its expert; the first
+    // stores complete before any thread passes the barrier, so a row's last store is its owner's
+    for (int i = tid; i < a.T; i += NT) *(int2*)(a.row_info + 2 * i) = make_int2(-1, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int c = tid; c < nch; c += NT) {
+        const int4 en = ent[c];
+        for (int r = 0; r < en.z; ++r) a.row_info[2 * (en.y + r)] = en.x;
+    }
 }
+__global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) { plan_body<1024>(a); }
+
+
 
 // had128 over 128-blocks held 8 consecutive elements a lane: lane l of a 16-lane row holds the elements 8 g .. 8 g + 7
 // of its block, g = rot_group(l) = l ^ 3 where bit 2 of l is set, else l. The stages h = 1, 2, 4 run inside the lane;
@@ -1021,13 +1034,18 @@ __device__ __forceinline__ void load8w(const uint16_t* p, bool wide, uint32_t (&
 // written (nothing reads them); a negative sorted_tok gives zeros.
 constexpr int ROT_PASSES = 2;
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
+    if (a.plan && blockIdx.x == 0) {                              // the launch's first workgroup plans the GEMMs
+        plan_body<256>(a);
+        return;
+    }
     const int lane = threadIdx.x & 63;
+    const int gb = (int)blockIdx.x - (a.plan ? 1 : 0);
     const int nwg = (a.T + 3) / 4, per_xcd = (nwg + 7) / 8;
-    const int wg = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    const int wg = (gb & 7) * per_xcd + (gb >> 3);
     const int i = wg * 4 + (int)(threadIdx.x >> 6);
     if (wg >= nwg || i >= a.T) return;
     const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
-    const int e = a.row_info[2 * i];
+    const int e = owner_wave(a.off, a.n_expert, i, lane);       // the plan (beside) writes row_info later
     const int tok = a.sorted[i];
     if (e < 0) return;
     const Exl3c4Class& K = a.cls[class_of(a, e)];
@@ -1096,32 +1114,17 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     }
 }
 
-// Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows).
-__global__ __launch_bounds__(256) void k_zero_dead(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+// Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows): wave w of
+// workgroup z takes row z * waves + w: the workgroups from a.tail_from of the last GEMM's launch.
+__device__ __forceinline__ void zero_dead_rows(const Exl3c4Launch& a, int z) {
+    const int nw = (int)(blockDim.x >> 6), lane = threadIdx.x & 63;
+    const int64_t i = (int64_t)z * nw + (threadIdx.x >> 6);
     if (i >= a.T || a.row_info[2 * i] >= 0) return;
     uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
     for (int b = 0; b < a.nblk; ++b) {
         out[b * 128 + lane] = 0;
         out[b * 128 + lane + 64] = 0;
     }
-}
-
-// Each row's owner, by a binary search of the runs (clamped to [0, T)) per thread: row_info[i] = {e or -1, 0}.
-__global__ __launch_bounds__(256) void k_rowinfo(const Exl3c4Launch a) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= a.T) return;
-    // the last e with clamp(off[e]) <= i, over e in [0, n_expert)
-    int lo = 0, hi = a.n_expert - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (min(max(a.off[mid], 0), a.T) <= i) lo = mid;
-        else hi = mid - 1;
-    }
-    const int o0 = min(max(a.off[lo], 0), a.T), o1 = min(max(a.off[lo + 1], o0), a.T);
-    a.row_info[2 * i] = (o0 <= i && i < o1) ? lo : -1;
-    a.row_info[2 * i + 1] = 0;
 }
 
 // Stage one 128-k block of up to 64 rows of a row-major f16 source into LDS, permuted (perm_slot) so that each A
@@ -1278,11 +1281,15 @@ __device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class
 // its waves. With keep_sums the raw sums go to part (a checker's view). Then the accumulations cross LDS and each
 // wave finishes whole rows of the block: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step
 // f16(had(f16(h * dn_suh))) (kernels/exl3ref/ref.c:187-212) into y at columns 128 hb... A negative sorted_tok, and a
-// narrower class's blocks past its width, are written zero; rows no run holds are k_zero_dead's.
+// narrower class's blocks past its width, are written zero; rows no run holds are the tail workgroups'.
 template <int BITS, int CB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
     constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
+    if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // gate_up alone: the rows no run holds
+        zero_dead_rows(a, (int)blockIdx.x - a.tail_from);
+        return;
+    }
     int hb, chunk;
     if (!xcd_unit(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, hb, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1350,6 +1357,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
+    if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // the rows no run holds
+        zero_dead_rows(a, (int)blockIdx.x - a.tail_from);
+        return;
+    }
     int b, chunk;
     if (!xcd_unit(a.nblk, a.plan + EXL3C4_PF_XCD_DN, b, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1573,21 +1584,10 @@ extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, v
     return launched();
 }
 
-extern "C" int exl3c4_dev_rowinfo(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    if (a->T <= 0) return 0;
-    return go(k_rowinfo, (unsigned)((a->T + 255) / 256), (hipStream_t)stream, ev0, ev1, *a);
-}
-
 extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     if (a->T <= 0) return 0;
     const unsigned nwg = (unsigned)((a->T + 3) / 4);
-    return go(k_rot, 8 * ((nwg + 7) / 8), (hipStream_t)stream, ev0, ev1, *a);
-}
-
-extern "C" int exl3c4_dev_zero_dead(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const int64_t waves = a->nblk > 0 ? (int64_t)a->T : 0;
-    if (waves <= 0) return 0;
-    return go(k_zero_dead, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+    return go(k_rot, 8 * ((nwg + 7) / 8) + (a->plan ? 1 : 0), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 // The most chunks k_plan can deal one XCD: the midpoints of its chunks lie in a stretch of total / 8 (total <=
@@ -1598,11 +1598,14 @@ extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->n_grp < 2 || a->max_chunks <= 0) return 0;
-    const dim3 grid((unsigned)(8 * (a->n_grp / 2) * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_GU)));
+    Exl3c4Launch g = *a;
+    const int units = 8 * (a->n_grp / 2) * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_GU);
+    g.tail_from = a->tail_from ? units : 0;                       // then (T + 7) / 8 workgroups zero dead rows
+    const dim3 grid((unsigned)(units + (g.tail_from ? (a->T + 7) / 8 : 0)));
     if (ev0 && ev1)
-        hipExtLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, *a);
+        hipExtLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, g);
     else
-        hipLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, *a);
+        hipLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, g);
     return launched();
 }
 
@@ -1610,8 +1613,10 @@ extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     const GemmFn f = by_bits<DnPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
-    return go2(f, dim3((unsigned)(8 * a->nblk * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_DN))), (hipStream_t)stream, ev0, ev1,
-               0u, *a);
+    Exl3c4Launch g = *a;
+    const int units = 8 * a->nblk * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_DN);
+    g.tail_from = a->tail_from ? units : 0;                       // then (T + 3) / 4 workgroups zero dead rows
+    return go2(f, dim3((unsigned)(units + (g.tail_from ? (a->T + 3) / 4 : 0))), (hipStream_t)stream, ev0, ev1, 0u, g);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,

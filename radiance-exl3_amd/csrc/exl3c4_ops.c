@@ -313,22 +313,22 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     p.row_info = (int32_t*)(s + k->row_info);
     p.plan = (int32_t*)(s + k->plan);
     p.max_chunks = (int32_t)k->max_chunks;
-    if ((rc = exl3c4_dev_plan(&p, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
-    if ((rc = exl3c4_dev_rowinfo(&p, stream, NULL, NULL)) != 0) return rc;
 
     const void* gin = o->x;                       /* gate_up's GEMM input: xr */
     int64_t gin_pitch = o->x_pitch;
     const void* din = o->x;                       /* down's GEMM input: h, rotated */
     int64_t din_pitch = o->x_pitch;
-    if (k->xr_pitch) {
+    if (k->xr_pitch) {                            /* the rotation, its launch's last workgroup planning beside it */
         Exl3c4Launch r = p;
         for (int c = 0; c < o->n_class; ++c) r.cls[c] = o->cls[c];
         r.y = s + k->xr;
         r.y_pitch = k->xr_pitch;
         r.h_from_gu = op == EXL3C4_DOWN ? 1 : 2;  /* halves a row */
-        if ((rc = exl3c4_dev_rot(&r, stream, NULL, NULL)) != 0) return rc;
+        if ((rc = exl3c4_dev_rot(&r, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
         if (op == EXL3C4_DOWN) { din = s + k->xr; din_pitch = k->xr_pitch; }
         else { gin = s + k->xr; gin_pitch = k->xr_pitch; }
+    } else if ((rc = exl3c4_dev_plan(&p, stream, EV(EXL3C4_K_PREP))) != 0) {
+        return rc;
     }
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a = p;
@@ -340,9 +340,11 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
         a.h_rot = op == EXL3C4_GU_DN ? 1 : o->h_rot;
         if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
         else a.nblk = (int32_t)(o->y_cols / 128);
-        /* the GEMM with its epilogue: h (rotated for down when h_rot) for every row a chunk holds */
+        /* the GEMM with its epilogue: h (rotated for down when h_rot) for every row a chunk holds; gate_up alone
+         * also zeroes the rows no run holds, in workgroups after the GEMM's */
+        a.tail_from = op == EXL3C4_GATE_UP;
         if ((rc = exl3c4_dev_gu_pf(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
-        if (op == EXL3C4_GATE_UP) return exl3c4_dev_zero_dead(&a, stream, NULL, NULL);
+        if (op == EXL3C4_GATE_UP) return EXL3C4_OK;
         din = s + k->h;
         din_pitch = k->h_pitch;
     }
@@ -353,8 +355,8 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     d.nblk = (int32_t)(o->y_cols / 128);
     d.dacc = (float*)(s + k->dacc);
     d.dacc_pitch = k->dacc_pitch;
-    if ((rc = exl3c4_dev_dn_pf(&d, stream, EV(EXL3C4_K_DOWN))) != 0) return rc;
-    return exl3c4_dev_zero_dead(&d, stream, NULL, NULL);
+    d.tail_from = 1;                              /* and the rows no run holds, zeroed after the GEMM's workgroups */
+    return exl3c4_dev_dn_pf(&d, stream, EV(EXL3C4_K_DOWN));
 }
 
 /* gate_up_down at decode as one kernel: the row counters and status zeroed (or the caller's zeroed block taken), then
