@@ -246,17 +246,6 @@ __device__ __forceinline__ void decode_segment(const uint32_t (&d)[BITS], uint32
     decode_seg_impl<BITS, CB>(v, B, k, std::make_integer_sequence<int, 16>{});
 }
 
-// Quarter QT of a segment's decode: positions 8 QT .. 8 QT + 7 (four pairs).
-template <int BITS, int CB, int QT, int... P>
-__device__ __forceinline__ void decode_quarter_impl(const uint32_t (&v)[BITS + 1], uint32_t (&B)[16],
-                                                    const Mul1Consts& k, std::integer_sequence<int, P...>) {
-    (decode_pair<BITS, CB, 8 * QT + 2 * P>(v, B, k), ...);
-}
-template <int BITS, int CB, int QT>
-__device__ __forceinline__ void decode_quarter(const uint32_t (&v)[BITS + 1], uint32_t (&B)[16], const Mul1Consts& k) {
-    decode_quarter_impl<BITS, CB, QT>(v, B, k, std::make_integer_sequence<int, 4>{});
-}
-
 // A lane's K words of one block: K u32 at p (4-byte aligned).
 template <int BITS, typename P> __device__ __forceinline__ void load_words(P p, uint32_t (&d)[BITS]) {
     typedef __attribute__((address_space(1))) const u32x4a_t* q4p;
@@ -1174,54 +1163,30 @@ __device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, int& unit, 
     return chunk < xb[x + 1];
 }
 
-// One k-step of the prefill GEMM, software-pipelined by a step: the MFMAs of step ks (B operands Bc, decoded a step
-// earlier) tile by tile, each tile's four followed by a quarter of step ks + 1's decode (code dn) into Bn. The wave
-// issues that decode while the matrix core runs the MFMAs; the next tile's A comes from LDS meanwhile. Every register
-// an MFMA reads stays live (an empty asm use) until the decode quarter after it has issued -- 30-odd VALU
-// instructions, well past the cycles in which the MFMA reads its A and B -- so nothing the compiler places there can
-// overwrite an operand still being read (gfx950 does not interlock a VALU write against an in-flight 16x16x32 MFMA's
-// A/B reads, and the compiler does not pad for it).
-template <int BITS, int CB, int NT, int T>
-__device__ __forceinline__ void pf_tile(const uint16_t* Ab, int kp, const half8_t (&bq)[4], half8_t& Aa,
-                                        half8_t& Ac, const uint32_t (&v)[BITS + 1], uint32_t (&Bn)[16],
-                                        const Mul1Consts& k, float4_t (&acc)[4][2]) {
-    if constexpr (T < NT) {
-        acc[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, bq[0], acc[T][0], 0, 0, 0);
-        acc[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, bq[1], acc[T][1], 0, 0, 0);
-        acc[T][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, bq[2], acc[T][0], 0, 0, 0);
-        acc[T][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, bq[3], acc[T][1], 0, 0, 0);
-    }
-    half8_t Na, Nc;
-    if constexpr (T + 1 < NT) {                                   // the next tile's A
-        const uint16_t* arow = Ab + 16 * kp;
-        Na = *(const half8_t*)arow;
-        Nc = *(const half8_t*)(arow + 8);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    decode_quarter<BITS, CB, T>(v, Bn, k);
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (T < NT) asm volatile("" ::"v"(Aa), "v"(Ac));
-    if constexpr (T + 1 < NT) { Aa = Na; Ac = Nc; }
-}
+// One k-step of the prefill GEMM: the step's B operands (decoded just before) against each of the chunk's NT row
+// tiles (4 MFMAs a tile), each group ending in mfma_guard: gfx950 does not interlock a VALU or LDS write against an
+// in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (The MFMAs do not overlap the decode's
+// VALU work anyway -- measured: a mix of both in one wave costs about their sum -- so a step issued behind its
+// decode gains nothing and costs a second set of B registers.)
 template <int BITS, int CB, int NT>
-__device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&Bc)[16],
-                                        const uint32_t (&dn)[BITS], uint32_t (&Bn)[16], const Mul1Consts& k,
-                                        float4_t (&acc)[4][2]) {
-    uint32_t v[BITS + 1];
-    segment_window<BITS>(dn, v);
-    const half8_t bq[4] = { as_half8(Bc[0], Bc[1], Bc[2], Bc[3]), as_half8(Bc[8], Bc[9], Bc[10], Bc[11]),
-                            as_half8(Bc[4], Bc[5], Bc[6], Bc[7]), as_half8(Bc[12], Bc[13], Bc[14], Bc[15]) };
-    half8_t Aa = *(const half8_t*)Ab, Ac = *(const half8_t*)(Ab + 8);
-    pf_tile<BITS, CB, NT, 0>(Ab, kp, bq, Aa, Ac, v, Bn, k, acc);
-    pf_tile<BITS, CB, NT, 1>(Ab + 16 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
-    pf_tile<BITS, CB, NT, 2>(Ab + 32 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
-    pf_tile<BITS, CB, NT, 3>(Ab + 48 * kp, kp, bq, Aa, Ac, v, Bn, k, acc);
-    asm volatile("" ::"v"(bq[0]), "v"(bq[1]), "v"(bq[2]), "v"(bq[3]));
+__device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[4][2]) {
+    const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
+    const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint16_t* arow = Ab + t * 16 * kp;
+        const half8_t Aa = *(const half8_t*)arow, Ac = *(const half8_t*)(arow + 8);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b0, acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Aa, b1, acc[t][1], 0, 0, 0);
+        acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b2, acc[t][0], 0, 0, 0);
+        acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ac, b3, acc[t][1], 0, 0, 0);
+        mfma_guard(Aa, Ac, b0, b1, b2, b3);
+    }
 }
 
 // The prefill GEMM of one chunk (<= 64 rows of one expert) against the strips of one workgroup, all of k: the input's
 // 128-k blocks stream through two LDS buffers a half; each wave decodes its strip's step once and runs it against every
-// row tile, a step behind its decode (pf_step). NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8
+// row tile (pf_step). NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8
 // waves, two staged inputs (columns k and half_off + k), thread t staging half t / 256 and wave w reading half w / 4.
 // NT: the chunk's 16-row tiles (ceil(nrows / 16)), a template argument so that the loop holds no branch on it.
 // Accumulations: acc[row tile][strip half].
@@ -1236,7 +1201,7 @@ __device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Cl
     const int scol = col_off + sh * half_off;                     // this thread's staged input column
     auto bufp = [&](int b, int h) { return lds + (b * NH + h) * 64 * kp; };
     const gu32p rec = (gu32p)tab_entry(W.codes, W.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
-    // the codes of the steps ahead: dA even steps, dB odd; each refill 3 steps ahead of the step it serves (clamped:
+    // the codes of the steps ahead: dA even steps, dB odd; each refill 2 steps ahead of the step it serves (clamped:
     // past the stream a harmless reload of the last step, unconditional so that the waits count exactly)
     uint32_t dA[BITS], dB[BITS];
     load_words<BITS>(rec, dA);
@@ -1244,9 +1209,6 @@ __device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Cl
     StageRegs r;
     stage_load(src, pitch, row0, nrows, scol, r, tid);
     const Mul1Consts k = mul1_consts();
-    uint32_t B0[16], B1[16];                                      // the decoded steps: even in B0, odd in B1
-    decode_segment<BITS, CB>(dA, B0, k);
-    load_words<BITS>(rec + (int64_t)min(2, ksteps - 1) * 64 * BITS, dA);
     stage_store(bufp(0, sh), kp, r, tid);
     __syncthreads();
     const int rr = lane & 15, g = lane >> 4;
@@ -1255,10 +1217,15 @@ __device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Cl
         stage_load(src, pitch, row0, nrows, scol + min(kb + 1, nb - 1) * 128, r, tid);
         const uint16_t* Ab = bufp(kb & 1, sh) + rr * kp + 16 * g;
         const int ks = 2 * kb;
-        pf_step<BITS, CB, NT>(Ab, kp, B0, dB, B1, k, acc);       // step ks; decodes ks + 1
-        load_words<BITS>(rec + (int64_t)min(ks + 3, ksteps - 1) * 64 * BITS, dB);
-        pf_step<BITS, CB, NT>(Ab + EXL3C4_KSTEP, kp, B1, dA, B0, k, acc);   // step ks + 1; decodes ks + 2
-        load_words<BITS>(rec + (int64_t)min(ks + 4, ksteps - 1) * 64 * BITS, dA);
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            uint32_t B[16];
+            decode_segment<BITS, CB>(s2 ? dB : dA, B, k);
+            const int nx = min(ks + s2 + 2, ksteps - 1);
+            if (s2 == 0) load_words<BITS>(rec + (int64_t)nx * 64 * BITS, dA);
+            else load_words<BITS>(rec + (int64_t)nx * 64 * BITS, dB);
+            pf_step<BITS, CB, NT>(Ab + s2 * EXL3C4_KSTEP, kp, B, acc);
+        }
         if (kb + 1 < nb) stage_store(bufp((kb + 1) & 1, sh), kp, r, tid);
         __syncthreads();
     }
