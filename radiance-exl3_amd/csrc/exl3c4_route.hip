@@ -43,6 +43,38 @@ struct Pick { int id; float w; };
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int d) {
     return ((uint64_t)(uint32_t)__shfl_xor((int)(v >> 32), d) << 32) | (uint64_t)(uint32_t)__shfl_xor((int)(uint32_t)v, d);
 }
+// The value of lane l ^ J, without the LDS pipe's bpermute: DPP moves for J = 1, 2 (quad_perm) and 8 (row_ror 8), a
+// ds_swizzle (xor mode, within 32 lanes) for 4, gfx950's permlane swaps for 16 and 32 (each lane takes the half of
+// the swapped pair that came from its partner). Every lane of the wave must be active.
+template <int J> __device__ __forceinline__ uint32_t xor_lane(uint32_t v, int lane) {
+    if constexpr (J == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (J == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (J == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x101F);
+    else if constexpr (J == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x128, 0xF, 0xF, false);
+    else if constexpr (J == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+template <int J> __device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int lane) {
+    return ((uint64_t)xor_lane<J>((uint32_t)(v >> 32), lane) << 32) | (uint64_t)xor_lane<J>((uint32_t)v, lane);
+}
+template <int J> __device__ __forceinline__ float xor_lanef(float v, int lane) {
+    return __uint_as_float(xor_lane<J>(__float_as_uint(v), lane));
+}
+__device__ __forceinline__ uint64_t xor_lane64_rt(uint64_t v, int j, int lane) {   // j a power of two <= 32
+    switch (j) {
+    case 1: return xor_lane64<1>(v, lane);
+    case 2: return xor_lane64<2>(v, lane);
+    case 4: return xor_lane64<4>(v, lane);
+    case 8: return xor_lane64<8>(v, lane);
+    case 16: return xor_lane64<16>(v, lane);
+    default: return xor_lane64<32>(v, lane);
+    }
+}
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
@@ -53,7 +85,7 @@ __device__ __forceinline__ uint64_t sort_desc(uint64_t v, int lane) {
     for (int k = 2; k <= 64; k <<= 1)
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint64_t o = shfl_xor64(v, j);
+            const uint64_t o = xor_lane64_rt(v, j, lane);        // j is a constant once unrolled
             const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
             v = take_max ? (o > v ? o : v) : (o < v ? o : v);
         }
@@ -84,8 +116,12 @@ __device__ __forceinline__ Pick route_token(const void* logits, int64_t row, int
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) m = fmaxf(m, v[j]);              // a NaN never wins
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d));
+    m = fmaxf(m, xor_lanef<32>(m, lane));
+    m = fmaxf(m, xor_lanef<16>(m, lane));
+    m = fmaxf(m, xor_lanef<8>(m, lane));
+    m = fmaxf(m, xor_lanef<4>(m, lane));
+    m = fmaxf(m, xor_lanef<2>(m, lane));
+    m = fmaxf(m, xor_lanef<1>(m, lane));
     float s = 0.f;
     uint64_t key[RPL];
 #pragma unroll
@@ -94,8 +130,12 @@ __device__ __forceinline__ Pick route_token(const void* logits, int64_t row, int
         s = s + (in ? expf(v[j] - m) : 0.f);
         key[j] = in ? rank_key(v[j], lane + 64 * j) : 0ull;     // 0: below every real key
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) s = s + __shfl_xor(s, d);
+    s = s + xor_lanef<32>(s, lane);                               // the butterfly, partners 32, 16, .., 1
+    s = s + xor_lanef<16>(s, lane);
+    s = s + xor_lanef<8>(s, lane);
+    s = s + xor_lanef<4>(s, lane);
+    s = s + xor_lanef<2>(s, lane);
+    s = s + xor_lanef<1>(s, lane);
 
     // The top_k keys are all at least thr, the top_k-th largest of the lanes' own largest keys (top_k lanes hold a key
     // that large). Those candidates -- at most 64 on this path -- are gathered one a lane and sorted; lane r then
@@ -134,7 +174,7 @@ __device__ __forceinline__ Pick route_token(const void* logits, int64_t row, int
     }
     const float p = lane < top_k ? expf(key_logit(mykey) - m) / s : 0.f;
     float psum = 0.f;
-    for (int r = 0; r < top_k; ++r) psum = psum + __shfl(p, r);   // in rank order
+    for (int r = 0; r < top_k; ++r) psum = psum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_int(p), r));   // rank order
     return Pick{ (int)(0xFFFFFFFFu - (uint32_t)mykey), renorm ? p / psum : p };
 }
 
@@ -253,6 +293,62 @@ __global__ __launch_bounds__(512) void k_scatter(const int32_t* ids, int32_t T, 
     scatter_body(ids, T, base, n_expert, sorted, off, count, row_of, sc_lds, sc_lds + SC_WAVES * n_expert);
 }
 
+// moe_scatter of at most blockDim.x pairs whose ids sit in LDS (16-byte aligned, room for T rounded up to 4), for
+// at most blockDim.x experts: a histogram (LDS atomics), expert_offset its exclusive scan (a wave scan, then the waves'
+// totals), and pair i's row = offset of its expert + the number of earlier pairs with the same expert (the stable
+// counting sort's row; only the pair threads count, over the ids before theirs, four at a time). lds: n_expert + 1 +
+// 16 ints.
+__device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int n_expert, int32_t* sorted, int32_t* off,
+                                              int32_t* count, int32_t* row_of, int* lds) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    int* cnt = lds;                                               // [n_expert]: counts, then exclusive offsets
+    int* wsum = lds + n_expert + 1;                               // [16]: the waves' totals
+    if (tid < n_expert) cnt[tid] = 0;
+    __syncthreads();
+    int e = -1, w = 0;
+    if (tid < T) {
+        const int f = ids_l[tid];
+        e = (f >= 0 && f < n_expert) ? f : -1;
+        if (e >= 0) {
+            atomicAdd(&cnt[e], 1);
+            for (int j0 = 0; j0 < tid; j0 += 4) {                // earlier pairs of the same expert
+                const int4 q = *(const int4*)(ids_l + j0);
+                w += (q.x == e) + (j0 + 1 < tid && q.y == e) + (j0 + 2 < tid && q.z == e) + (j0 + 3 < tid && q.w == e);
+            }
+        }
+    }
+    __syncthreads();
+    const int c = tid < n_expert ? cnt[tid] : 0;
+    int incl = c;                                                 // inclusive scan across the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) wsum[wv] = incl;
+    __syncthreads();
+    int base = 0, live = 0;
+    for (int u = 0; u < (int)(blockDim.x >> 6); ++u) {
+        const int t = wsum[u];
+        base += u < wv ? t : 0;
+        live += t;
+    }
+    if (tid < n_expert) {
+        const int ex = base + incl - c;
+        off[tid] = ex;
+        if (count) count[tid] = c;
+        cnt[tid] = ex;                                            // this thread alone read cnt[tid] above
+    }
+    if (tid == 0) off[n_expert] = live;
+    __syncthreads();
+    if (tid < T) {
+        const int rank = e >= 0 ? cnt[e] + w : -1;
+        if (e >= 0) sorted[rank] = tid;
+        if (row_of) row_of[tid] = rank;
+    }
+    for (int i = live + tid; i < T; i += blockDim.x) sorted[i] = -1;
+}
+
 // router_topk_scatter (the two fused, as the contract names them, include/exl3_abi.h:96-98) for at most 16 tokens, in
 // one workgroup of 16 waves: wave t routes token t, its ids go to LDS as well, then the scatter reads them there.
 template <int DT, int RPL>
@@ -260,7 +356,7 @@ __global__ __launch_bounds__(1024) void k_route_scatter(const void* logits, int3
                                                         int64_t pitch, int32_t top_k, int32_t renorm, int32_t* ids,
                                                         float* w, int32_t* sorted, int32_t* off, int32_t* count,
                                                         int32_t* row_of) {
-    extern __shared__ int rs_lds[];
+    extern __shared__ __attribute__((aligned(16))) int rs_lds[];   // ids first: 16-byte reads
     __shared__ uint64_t cand[16][64];
     int* ids_l = rs_lds;                                          // [16 * 64]
     int* cnt = rs_lds + 16 * 64;
@@ -274,7 +370,9 @@ __global__ __launch_bounds__(1024) void k_route_scatter(const void* logits, int3
         }
     }
     __syncthreads();
-    scatter_body(ids_l, n_tok * top_k, 0, n_expert, sorted, off, count, row_of, cnt, cnt + SC_WAVES * n_expert);
+    if (n_tok * top_k <= (int)blockDim.x && n_expert <= (int)blockDim.x)
+        scatter_small(ids_l, n_tok * top_k, n_expert, sorted, off, count, row_of, cnt);
+    else scatter_body(ids_l, n_tok * top_k, 0, n_expert, sorted, off, count, row_of, cnt, cnt + SC_WAVES * n_expert);
 }
 
 // moe_gather: one thread a run of 8 columns of one token; the slots in ascending order, one f32 product and one add
@@ -382,7 +480,8 @@ extern "C" int exl3c4_dev_route_scatter(const void* logits, int32_t dtype, int32
                                         int64_t pitch, int32_t top_k, int32_t renorm, int32_t* ids, float* w,
                                         int32_t* sorted, int32_t* off, int32_t* count, int32_t* row_of,
                                         void* stream) {
-    const uint32_t lds = (uint32_t)((16 * 64 + SC_WAVES * n_expert + SC_WAVES) * 4);
+    const int tail = SC_WAVES * n_expert + SC_WAVES > n_expert + 17 ? SC_WAVES * n_expert + SC_WAVES : n_expert + 17;
+    const uint32_t lds = (uint32_t)((16 * 64 + tail) * 4);       // ids, then scatter_body's or scatter_small's
     const hipStream_t st = (hipStream_t)stream;
     if (dtype == EXL3C4_F32)
         launch_rs_dt<EXL3C4_F32>(logits, n_tok, n_expert, pitch, top_k, renorm, ids, w, sorted, off, count, row_of, lds, st);
