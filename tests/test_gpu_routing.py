@@ -95,18 +95,20 @@ def test_scatter_matches_the_oracle(torch_cuda, n_tok, top_k, n_expert, base, ki
         assert np.array_equal(g, w_), name
 
 
-@pytest.mark.parametrize("n_tok", [8, 16, 40])
-def test_router_topk_scatter_matches_the_oracle(torch_cuda, n_tok):
+@pytest.mark.parametrize("n_tok,E,top_k", [(8, 512, 10), (16, 512, 10), (40, 512, 10), (16, 8, 4), (16, 1024, 64),
+                                            (3, 1, 1), (16, 64, 64), (5, 100, 7)])
+def test_router_topk_scatter_matches_the_oracle(torch_cuda, n_tok, E, top_k):
     """The fused entry (one workgroup up to 16 tokens, the two launches beyond) against the oracle's router then
-    scatter."""
+    scatter: many pairs an expert (8 experts), the most experts and pairs one workgroup scatters (1024 and 16 x 64),
+    one expert, top_k = n_expert, an n_expert off the powers of two."""
     import exl3c4
     import oracle
     torch = torch_cuda
-    E, top_k = 512, 10
-    print(f"router_topk_scatter {n_tok} tokens", flush=True)
+    print(f"router_topk_scatter {n_tok} tokens, {E} experts, top_k {top_k}", flush=True)
     rng = np.random.default_rng(100 + n_tok)
     lg = rng.standard_normal((n_tok, E)).astype(np.float32)
-    lg[1] = np.round(lg[1] * 2) / 2                              # ties
+    if n_tok > 1:
+        lg[1] = np.round(lg[1] * 2) / 2                          # ties
     T = n_tok * top_k
     ids = torch.full((n_tok, top_k), -7, dtype=torch.int32, device="cuda")
     w = torch.full((n_tok, top_k), -7.0, dtype=torch.float32, device="cuda")
