@@ -1276,6 +1276,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     const int half = wave >> 2, strip = half ? N / 64 + 4 * hb + (wave & 3) : 4 * hb + wave;
+    const int srt = a.sorted[row0 + min(lane, nrows - 1)];        // the chunk's sorted_tok, lane q row q (readlane)
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
@@ -1307,7 +1308,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     for (int row = wave; row < nrows; row += 8) {
         const int64_t r = row0 + row;
         uint16_t v0 = 0, v1 = 0;
-        if (a.sorted[r] >= 0) {
+        if (__builtin_amdgcn_readlane(srt, row) >= 0) {
             const float* p = acc_l + row * ACC_PITCH;
             const float ac[4] = { p[lane], p[lane + 64], p[128 + lane], p[192 + lane] };
             gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
@@ -1345,6 +1346,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
         return;
     }
+    const int srt = a.sorted[row0 + min(lane, nrows - 1)];        // the chunk's sorted_tok, lane q row q (readlane)
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
@@ -1376,7 +1378,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     dacc[lane + 64] = y1;
                 }
                 uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
-                if (a.sorted[r] < 0) {
+                if (__builtin_amdgcn_readlane(srt, row) < 0) {
                     out[lane] = 0;
                     out[lane + 64] = 0;
                 } else {
