@@ -180,7 +180,8 @@ def common(args, ms, steps, value, unit, workload, extra=None):
 def run_decode_layer(args, torch, exl3c4):
     """A step is the whole layer on the device: router_topk_scatter on the draw's logits (softmax over the 512 experts,
     top-10, renormalised; the stable scatter), one gate_up_down launch, and moe_gather (the weighted sum in f32, cast
-    to f16)."""
+    to f16), the gather riding in gate_up_down's kernel (exl3c4_launch_gather); the same step with the gather as its
+    own dispatch is timed beside it."""
     layers = build_layers(torch, args.layers, args.seed)
     draws = build_draws(torch, args.draws, args.seed + 1)
     T = M * TOP_K
@@ -207,8 +208,15 @@ def run_decode_layer(args, torch, exl3c4):
         D = draws[i % n % args.draws]
         check_rc(exl3c4, exl3c4.router_topk_scatter(D["logits"], TOP_K, True, ids, w, st_d, off_d, None, row_of,
                                                     stream))
+        check_rc(exl3c4, exl3c4.launch_gather(layer_ops[i % n], scratch, ctr, w, row_of, out_t, stream))
+
+    def layer_step_separate(i, stream):
+        D = draws[i % n % args.draws]
+        check_rc(exl3c4, exl3c4.router_topk_scatter(D["logits"], TOP_K, True, ids, w, st_d, off_d, None, row_of,
+                                                    stream))
         check_rc(exl3c4, exl3c4.launch_ctr(layer_ops[i % n], scratch, ctr, stream))
         check_rc(exl3c4, exl3c4.moe_gather(y, True, w, row_of, out_t, stream))
+    ms_sep = timed_graph(torch, layer_step_separate, args.steps, args.warmup)
     ms = timed_graph(torch, layer_step, args.steps, args.warmup)
     ms_op = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch_ctr(ops[i % n], scratch, ctr, st)),
                         args.steps, args.warmup)
@@ -233,6 +241,7 @@ def run_decode_layer(args, torch, exl3c4):
                   "mean_live_experts": round(float(np.mean(live)), 2)})
     out.update({
         "op_us": round(ms_op / args.steps * 1e3, 2),              # the gate_up_down launch alone, graph replay
+        "step_us_gather_separate": round(ms_sep / args.steps * 1e3, 2),   # the step with moe_gather dispatched alone
         "packed_weight_GBps": round(layer_gbps, 1),
         "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",

@@ -114,7 +114,7 @@ int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* ro
 int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream);
 
 /* gate_up_down's single kernel (the decode path from EXL3C4_GD_FUSE_MIN_T sorted rows) orders its workgroups through
- * a block of counters -- a status word and two counters a sorted row -- that must be zero when it starts and that it
+ * a block of counters -- a status word and two counters a sorted row (and a line a token for exl3c4_launch_gather) -- that must be zero when it starts and that it
  * leaves zero again when it ends well (each row's last down unit zeroes the row's). exl3c4_launch zeroes them in its
  * scratch before every launch (one more dispatch). exl3c4_launch_ctr takes them from `ctr` instead: a device block of
  * at least exl3c4_ctr_bytes, 256-B aligned, that the caller zeroed once (hipMemset) and keeps -- the reference's
@@ -126,6 +126,18 @@ int exl3c4_launch(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void
 int64_t exl3c4_ctr_bytes(const Exl3c4Op* op);
 int exl3c4_launch_ctr(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
                       int64_t ctr_bytes);
+
+/* exl3c4_launch_ctr, then moe_gather of its output: exactly exl3c4_launch_ctr(op, ...) followed by
+ * exl3c4_moe_gather(op->y, EXL3C4_BF16, op->y_pitch, expert_w, row_of, op->M, op->top_k, op->y_cols, out, out_pitch)
+ * -- the same bits in y and out, and the same refusals. When gate_up_down runs as its single kernel and `ctr` is given
+ * (exl3c4_ctr_bytes covers a counter line a token after the rows'), the gather rides in that kernel: the down unit that
+ * completes a token's rows of a 128-column block sums that block, so the layer's step has no gather dispatch and no
+ * gather startup after the last down unit. Otherwise the two run one after the other. row_of must be the inverse of
+ * op->sorted_tok (what the scatter writes). op: gate_up_down or down. The reference's engine dispatches the two
+ * separately (include/exl3_abi.h:90-158); no counterpart there. */
+int exl3c4_launch_gather(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                         int64_t ctr_bytes, const float* expert_w, const int32_t* row_of, void* out,
+                         int64_t out_pitch);
 
 /* The kernels a launch can run: prep_gu's rotation; gate_up's GEMM (with its input rotation), then for gate_up alone
  * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums); and

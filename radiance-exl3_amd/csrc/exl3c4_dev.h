@@ -67,6 +67,14 @@ typedef struct Exl3c4Launch {
     int32_t        keep_sums;     /* prefill: also leave the GEMMs' f32 sums in part / dacc (a checker's view) */
     int32_t        tail_from;     /* prefill GEMMs: nonzero asks for workgroups that zero the rows no run holds after
                                      the GEMM's (the launcher sets where they start) */
+    /* gate_up_down in one launch with moe_gather behind it (g_out non-null): out[t] = f16(sum over the token's slots
+     * of expert_w x y[row_of]); token t's counter of 128-block b at g_ctr[t * SYNC_STRIDE + b] (zero, left zero) */
+    const float*   g_w;
+    const int32_t* g_row_of;
+    uint16_t*      g_out;
+    int64_t        g_out_pitch;
+    int32_t        g_ntok;
+    int32_t*       g_ctr;
 } Exl3c4Launch;
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the

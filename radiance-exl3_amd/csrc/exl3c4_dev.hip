@@ -673,6 +673,99 @@ __device__ __forceinline__ void wait_gate_up(const Exl3c4Launch& a, int i) {
 // any narrowing). Every (row, block) of y is written once: a row no run holds, a negative sorted_tok and a narrower
 // class's tail as zero. Inside gate_up_down's single launch (FUSED) the workgroup finds the row's owner itself and
 // waits for the row's gate_up units before it reads their sums.
+// y's 128-block b of one row: coherent stores when the launch gathers (the gathering unit may sit on another XCD and
+// reads them with coherent loads once every unit of the token's rows has counted, after its stores completed)
+__device__ __forceinline__ void put_y(const Exl3c4Launch& a, uint16_t* out, int lane, uint16_t v0, uint16_t v1) {
+    if (a.g_out) {
+        __hip_atomic_store(out + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(out + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        out[lane] = v0;
+        out[lane + 64] = v1;
+    }
+}
+
+// moe_gather behind gate_up_down's single launch (g_out set): a down unit that has stored its chunk's rows of block b
+// counts each live row on its token's counter of block b; the count that completes a token (its slots with a row,
+// from row_of) gathers that token's block -- k_gather's sum: the slots in ascending order, one f32 product and one add
+// each, f16 -- over the rows' y read coherently, then sets the counter back to zero. No unit waits here. A chunk holds
+// a token at most once (its slots name distinct experts), at most 16 rows at decode.
+__device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
+    __shared__ int tok_s[64];
+    __shared__ int ntok_s;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");              // this thread's y stores are done
+    __syncthreads();
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (wave == 0) {
+        bool last = false;
+        int t = -1;
+        if (lane < nrows) {
+            const int p = a.sorted[i + lane];
+            t = p >= 0 ? p / a.top_k : -1;
+            if (t >= 0 && t < a.g_ntok) {
+                const int old = __hip_atomic_fetch_add(a.g_ctr + (int64_t)t * EXL3C4_SYNC_STRIDE + b, 1,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                int need = 0;                                     // read while the count is in flight
+                for (int s = 0; s < a.top_k; ++s) need += a.g_row_of[(int64_t)t * a.top_k + s] >= 0;
+                last = old == need - 1;
+            }
+        }
+        const uint64_t m = __ballot(last);
+        if (last) tok_s[__popcll(m & ((1ull << lane) - 1ull))] = t;
+        if (lane == 0) ntok_s = __popcll(m);
+    }
+    __syncthreads();
+    const int n = ntok_s;
+    for (int j = wave; j < n; j += (int)(blockDim.x >> 6)) {
+        const int64_t t = tok_s[j];
+        const int c = b * 128 + lane;
+        float acc0 = 0.f, acc1 = 0.f;
+        for (int s0 = 0; s0 < a.top_k; s0 += 16) {                // 16 slots' rows and weights, then their values
+            int r[16];
+            float w[16];
+            uint16_t q0[16], q1[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const int sl = min(s0 + u, a.top_k - 1);
+                r[u] = a.g_row_of[t * a.top_k + sl];
+                w[u] = a.g_w[t * a.top_k + sl];
+                if (s0 + u >= a.top_k || r[u] >= a.T) r[u] = -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const uint16_t* yr = (const uint16_t*)a.y + (int64_t)(r[u] < 0 ? 0 : r[u]) * a.y_pitch + c;
+                q0[u] = __hip_atomic_load(yr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                q1[u] = __hip_atomic_load(yr + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float p0 = w[u] * bf2f(q0[u]), p1 = w[u] * bf2f(q1[u]);
+                const float s0v = acc0 + p0, s1v = acc1 + p1;
+                acc0 = r[u] < 0 ? acc0 : s0v;                     // a pair without a row adds nothing
+                acc1 = r[u] < 0 ? acc1 : s1v;
+            }
+        }
+        uint16_t* o = a.g_out + t * a.g_out_pitch + c;
+        o[0] = f2h(acc0);
+        o[64] = f2h(acc1);
+        if (lane == 0)
+            __hip_atomic_store(a.g_ctr + t * EXL3C4_SYNC_STRIDE + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The gather's tokens with no slot holding a row (no unit counts them): out zero, as k_gather writes. Wave w of job z
+// takes token 4 z + w.
+__device__ __forceinline__ void gather_empty(const Exl3c4Launch& a, int z) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)z * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (t >= a.g_ntok) return;
+    for (int s = 0; s < a.top_k; ++s) {
+        const int r = a.g_row_of[t * a.top_k + s];
+        if (r >= 0 && r < a.T) return;
+    }
+    for (int c = lane; c < a.y_cols; c += 64) a.g_out[t * a.g_out_pitch + c] = 0;
+}
+
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -699,11 +792,9 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     const Exl3c4Class& D = a.cls[c];
     const int N = D.rows, KC = D.cols;
     if (b * 128 >= N) {                                           // a narrower class's tail
-        for (int q = wave; q < nrows; q += 4) {
-            uint16_t* out = (uint16_t*)a.y + (int64_t)(i + q) * a.y_pitch + b * 128;
-            out[lane] = 0;
-            out[lane + 64] = 0;
-        }
+        for (int q = wave; q < nrows; q += 4)
+            put_y(a, (uint16_t*)a.y + (int64_t)(i + q) * a.y_pitch + b * 128, lane, 0, 0);
+        if (FUSED && a.g_out) gather_count(a, i, nrows, b);
         return;
     }
     const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
@@ -785,14 +876,13 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         dacc[lane + 64] = y1;
         uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
         if (a.sorted[r] < 0) {
-            out[lane] = 0;
-            out[lane + 64] = 0;
+            put_y(a, out, lane, 0, 0);
             continue;
         }
         had128_wave(y0, y1, lane);
-        out[lane] = f2bf(y0 * h2f(sv0));
-        out[lane + 64] = f2bf(y1 * h2f(sv1));
+        put_y(a, out, lane, f2bf(y0 * h2f(sv0)), f2bf(y1 * h2f(sv1)));
     }
+    if (FUSED && a.g_out) gather_count(a, i, nrows, b);
 }
 
 template <int BITS, int CB>
@@ -853,6 +943,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
     }
     const int d = slot - rows * ugu;
     if (d < rows * a.nblk) dn_unit<BITS, CB, true>(a, d % a.nblk, xcd + 8 * (d / a.nblk), lds);
+    else if (a.g_out) gather_empty(a, 8 * (d - rows * a.nblk) + xcd);  // the grid's last slots of each XCD
 }
 
 __global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
@@ -1533,7 +1624,8 @@ extern "C" int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, voi
     if (!f) return EXL3C4_E_DTYPE;
     if (a->T <= 0 || a->n_grp <= 0 || a->nblk <= 0) return 0;
     const uint32_t gu_lds = (uint32_t)(16 * a->lds_pitch_gu * 2), dn_lds = dn_lds_bytes(a);
-    const int64_t per_xcd = (int64_t)((a->T + 7) / 8) * (((int64_t)a->n_grp << a->ksplit_log2) + a->nblk);
+    const int64_t per_xcd = (int64_t)((a->T + 7) / 8) * (((int64_t)a->n_grp << a->ksplit_log2) + a->nblk) +
+                            (a->g_out ? (a->g_ntok + 31) / 32 : 0);  /* gather_empty: 4 tokens a workgroup */
     return go2(f, dim3((unsigned)(8 * per_xcd)), (hipStream_t)stream, ev0, ev1, gu_lds > dn_lds ? gu_lds : dn_lds, *a);
 }
 

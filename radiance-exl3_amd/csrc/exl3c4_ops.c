@@ -361,7 +361,16 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
 
 /* gate_up_down at decode as one kernel: the row counters and status zeroed (or the caller's zeroed block taken), then
  * k_gd (gate_up units, then down units waiting on their row's counter; the row's last down unit zeroes its counters). */
-static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t, int32_t* ctr) {
+/* moe_gather riding in gate_up_down's single kernel (exl3c4_launch_gather) */
+typedef struct {
+    const float*   w;
+    const int32_t* row_of;
+    void*          out;
+    int64_t        out_pitch;
+} Gather;
+
+static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t, int32_t* ctr,
+                      const Gather* gx) {
     int rc;
     Exl3c4Launch g;
     base_args(o, k, s, &g);
@@ -382,6 +391,14 @@ static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, 
     } else {
         g.sync = (int32_t*)(s + k->sync);
         if ((rc = exl3c4_dev_fill(g.sync, (o->T + 1) * EXL3C4_SYNC_STRIDE, stream)) != 0) return rc;
+    }
+    if (gx) {                                     /* only with the caller's block: the token counters follow the rows' */
+        g.g_w = gx->w;
+        g.g_row_of = gx->row_of;
+        g.g_out = (uint16_t*)gx->out;
+        g.g_out_pitch = gx->out_pitch;
+        g.g_ntok = (int32_t)o->M;
+        g.g_ctr = ctr + (o->T + 1) * EXL3C4_SYNC_STRIDE;
     }
     return exl3c4_dev_gd(&g, stream, EV(EXL3C4_K_GATE_UP_DOWN));
 }
@@ -412,7 +429,7 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
  *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1)
  * Prefill (launch_prefill) plans 64-row chunks of one expert first and runs one GEMM kernel a projection. */
 static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t,
-                       int32_t* ctr) {
+                       int32_t* ctr, const Gather* gx) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     if ((rc = check(o)) != EXL3C4_OK) return rc;
@@ -431,7 +448,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     }
 
     if (k.pf) return launch_prefill(o, &k, s, stream, t);
-    if (k.gd1) return launch_gd1(o, &k, s, stream, t, ctr);
+    if (k.gd1) return launch_gd1(o, &k, s, stream, t, ctr, gx);
 
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
@@ -470,12 +487,12 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
 
 int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
     const Timed t = { -1, NULL, NULL, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
 }
 
 int exl3c4_launch_checked(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
     const Timed t = { -1, NULL, NULL, 1 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
 }
 
 int64_t exl3c4_ctr_bytes(const Exl3c4Op* o) {
@@ -486,7 +503,8 @@ int64_t exl3c4_ctr_bytes(const Exl3c4Op* o) {
     q.T = o->M * o->top_k;
     if ((rc = check(&q)) != EXL3C4_OK) return rc;
     const int64_t T = q.T > o->T ? q.T : o->T;
-    return q.op == EXL3C4_GU_DN ? ALIGN_UP((T + 1) * EXL3C4_SYNC_STRIDE * 4, 256) : 0;
+    /* the status word and a counter a row, then a counter line a token (exl3c4_launch_gather) */
+    return q.op == EXL3C4_GU_DN ? ALIGN_UP((T + 1 + o->M) * EXL3C4_SYNC_STRIDE * 4, 256) : 0;
 }
 
 int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
@@ -499,7 +517,34 @@ int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, v
     if (k.gd1 && ctr && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
         return EXL3C4_E_SCRATCH;
     const Timed t = { -1, NULL, NULL, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL, NULL);
+}
+
+int exl3c4_launch_gather(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                         int64_t ctr_bytes, const float* expert_w, const int32_t* row_of, void* out, int64_t out_pitch) {
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
+    if (o->op != EXL3C4_GU_DN && o->op != EXL3C4_DOWN) return EXL3C4_E_INVAL;   /* y must be down's bf16 output */
+    if (!expert_w || !row_of || !out) return EXL3C4_E_INVAL;
+    if (out_pitch < o->y_cols) return EXL3C4_E_STRIDE;                         /* exl3c4_moe_gather's refusals */
+    if ((uintptr_t)o->y % 16 || (o->y_pitch * 2) % 16 || (uintptr_t)out % 16 || (out_pitch * 2) % 16 ||
+        (uintptr_t)expert_w % 4 || (uintptr_t)row_of % 4)
+        return EXL3C4_E_ALIGN;
+    Carve k;
+    carve(o, o->T, &k);
+    const int fuse = k.gd1 && ctr && o->y_cols / 128 <= EXL3C4_SYNC_STRIDE;
+    if (fuse && (ctr_bytes < (o->T + 1 + o->M) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
+        return EXL3C4_E_SCRATCH;
+    if (k.gd1 && ctr && !fuse && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
+        return EXL3C4_E_SCRATCH;
+    const Timed t = { -1, NULL, NULL, 0 };
+    const Gather gx = { expert_w, row_of, out, out_pitch };
+    if (fuse) return launch_impl(o, scratch, scratch_bytes, stream, &t, (int32_t*)ctr, &gx);
+    if ((rc = launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL, NULL)) != EXL3C4_OK)
+        return rc;
+    return exl3c4_moe_gather(o->y, EXL3C4_BF16, o->y_pitch, expert_w, row_of, o->M, o->top_k, o->y_cols, out,
+                             out_pitch, stream);
 }
 
 int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
@@ -511,7 +556,7 @@ int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes,
     carve(o, o->T, &k);
     if (!runs_kernel(o, &k, kernel)) return EXL3C4_E_INVAL;
     const Timed t = { kernel, ev_start, ev_stop, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL);
+    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
 }
 
 int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,

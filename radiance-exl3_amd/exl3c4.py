@@ -82,6 +82,8 @@ def lib():
         L.exl3c4_ctr_bytes.argtypes = [C.POINTER(Op)]
         L.exl3c4_launch_ctr.restype = C.c_int
         L.exl3c4_launch_ctr.argtypes = [C.POINTER(Op), _p, _i64, _p, _p, _i64]
+        L.exl3c4_launch_gather.restype = C.c_int
+        L.exl3c4_launch_gather.argtypes = [C.POINTER(Op), _p, _i64, _p, _p, _i64, _p, _p, _p, _i64]
         L.exl3c4_scratch_status.restype = C.c_int
         L.exl3c4_scratch_status.argtypes = [C.POINTER(Op), C.POINTER(_i64)]
         L.exl3c4_build_target.restype = C.c_char_p
@@ -247,6 +249,15 @@ def launch_ctr(o: Op, scratch, ctr, stream=None) -> int:
     n = 0 if scratch is None else scratch.numel()
     m = 0 if ctr is None else ctr.numel()
     return int(lib().exl3c4_launch_ctr(C.byref(o), _ptr(scratch), n, _stream(stream), _ptr(ctr), m))
+
+
+def launch_gather(o: Op, scratch, ctr, w, row_of, out, stream=None) -> int:
+    """exl3c4_launch_gather: launch_ctr, then moe_gather of the op's y (bf16) into out (int16 bits [n_tok, cols], f16)
+    with w f32 [n_tok, top_k] and row_of i32; the gather rides in gate_up_down's single kernel when it runs one."""
+    n = 0 if scratch is None else scratch.numel()
+    m = 0 if ctr is None else ctr.numel()
+    return int(lib().exl3c4_launch_gather(C.byref(o), _ptr(scratch), n, _stream(stream), _ptr(ctr), m, _ptr(w),
+                                          _ptr(row_of), _ptr(out), out.stride(0)))
 
 
 def partial_sums(o: Op, scratch, gemm: int = 0):

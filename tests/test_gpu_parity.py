@@ -258,3 +258,59 @@ def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bit
         torch.cuda.synchronize()
         assert int(torch.count_nonzero(ctr)) == 0, f"seed {seed}: the counter block is not zero after the launch"
         assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+
+
+# ------------------------------------------------------------------------------------------ the gather in the op's kernel
+@pytest.mark.parametrize("seed,n_tok,top_k,n_expert,geoms,drop,empty", [
+    (80, 8, 10, 96, [(512, 256)], 0.05, False),                 # one kernel, dropped pairs
+    (81, 6, 8, 40, [(512, 256), (256, 128)], 0.0, False),       # two classes: the narrower one's blocks are zero
+    (82, 8, 10, 96, [(512, 256)], 0.0, True),                   # a token whose slots all drop
+    (83, 5, 8, 12, [(256, 128)], 0.1, False),                   # few experts: chunks of several rows
+    (84, 2, 8, 12, [(256, 128)], 0.0, False),                   # T = 16: two kernels, then the gather's own
+])
+def test_launch_gather_gives_the_bits_of_the_launch_and_the_gather(torch_cuda, seed, n_tok, top_k, n_expert, geoms,
+                                                                   drop, empty):
+    """exl3c4_launch_gather: y and out bit for bit those of exl3c4_launch followed by exl3c4_moe_gather, out those of
+    the oracle's gather over the oracle's y; the counter block zero after each of two launches in a row (the second
+    with fewer tokens)."""
+    import exl3c4 as ex
+    import oracle
+    torch = torch_cuda
+    ctr = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    for rep, nt in enumerate((n_tok, max(1, n_tok - 3))):
+        ids = None
+        if empty:
+            rng0 = np.random.default_rng(seed)
+            ids = np.stack([rng0.permutation(n_expert)[:top_k] for _ in range(nt)]).astype(np.int32)
+            ids[nt // 2] = -1
+        case = Case(seed=seed + 100 * rep, n_tok=nt, top_k=top_k, n_expert=n_expert, geoms=geoms, bits=4, cb="mul1",
+                    drop=drop, expert_ids=ids)
+        dev = Dev(case)
+        want_y = dev.gate_up_down()
+        assert dev.status in (0, None)                            # None: fewer rows than the one-kernel path takes
+        N = max(d["rows"] for d in dev.tabs["dn"])
+        dn = [ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in dev.tabs["dn"]]
+        _, _, _, row_of = oracle.moe_scatter_full(case.ids, n_expert)
+        w = np.random.default_rng(seed + 7).random((nt, top_k)).astype(np.float32)
+        wt, rt = torch.from_numpy(w).cuda(), torch.from_numpy(row_of).cuda()
+        outs, ys = [], []
+        for fused in (True, False):
+            y = dev.out(N, fill=0x1234)
+            out = torch.full((nt, N), 0x1234, dtype=torch.int16, device="cuda")
+            o = ex.make_op(ex.GU_DN, case.bits, case.cb, dev.cls("gu"), dev.x, dev.sorted_tok, dev.off, y, nt,
+                           case.top_k, dn=dn)
+            s = ex.alloc_scratch(o)
+            print(f"launch_gather seed {seed} rep {rep} T {case.T} fused {fused}", flush=True)
+            if fused:
+                assert ctr.numel() >= ex.ctr_bytes(o)
+                assert ex.launch_gather(o, s, ctr, wt, rt, out) == 0
+            else:
+                assert ex.launch(o, s) == 0
+                assert ex.moe_gather(y, True, wt, rt, out) == 0
+            torch.cuda.synchronize()
+            ys.append(y.cpu().numpy().view(np.uint16))
+            outs.append(out.cpu().numpy().view(np.uint16))
+        assert int(torch.count_nonzero(ctr)) == 0, "the counter block is not zero after the launch"
+        assert np.array_equal(ys[0], want_y) and np.array_equal(ys[1], want_y)
+        assert np.array_equal(outs[0], outs[1])
+        assert np.array_equal(outs[0], oracle.moe_gather(want_y, True, w, row_of, nt, top_k))

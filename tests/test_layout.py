@@ -149,3 +149,21 @@ def test_scratch_is_sized_from_the_parameters_alone():
     assert exl3c4.scratch_bytes(o) == n1 and n1 > 0
     assert exl3c4.scratch_bytes(_op(M=16, top_k=10, E=64)) > n1
     assert exl3c4.scratch_bytes(_op(bits=9)) == -2
+
+
+def test_launch_gather_refuses_like_launch_and_moe_gather():
+    L = exl3c4.lib()
+    w, r, out = C.c_void_p(0x20000), C.c_void_p(0x30000), C.c_void_p(0x40000)
+
+    def rc(o, out_=out, pitch=256, w_=w):
+        return L.exl3c4_launch_gather(C.byref(o), None, 0, None, None, 0, w_, r, out_, pitch)
+    assert rc(_op(op=exl3c4.GU_DN, bits=9)) == -2             # the op's own refusals first
+    assert rc(_op(op=exl3c4.GATE_UP)) == -12                  # y must be down's output
+    assert rc(_op(op=exl3c4.GU_DN), w_=None) == -12
+    assert rc(_op(op=exl3c4.GU_DN), pitch=128) == -4          # moe_gather's: out narrower than y
+    assert rc(_op(op=exl3c4.GU_DN), out_=C.c_void_p(0x40008)) == -3
+    assert rc(_op(op=exl3c4.GU_DN), w_=C.c_void_p(0x20002)) == -3
+    assert rc(_op(op=exl3c4.GU_DN)) == -20                    # then the scratch
+    o = _op(op=exl3c4.GU_DN, M=8, top_k=10, E=64)
+    assert exl3c4.ctr_bytes(o) >= (80 + 1 + 8) * 256          # a counter line a row and a token
+
