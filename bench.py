@@ -235,8 +235,8 @@ def run_decode_layer(args, torch, exl3c4):
     out = common(args, ms, args.steps, M * args.steps / (ms / 1e3), "tokens/s",
                  "configs[2]: routed MoE layer decode, 512 experts (gate/up 2048->2x512, down 512->2048) at 4 bpw "
                  "mul1, 8 tokens; a step is the whole layer on the device: router_topk_scatter (softmax over N(0,1) "
-                 "logits, top-10, renormalised, stable scatter), one moe_exl3_gate_up_down launch, moe_gather (f32 "
-                 "weighted sum, f16 out)",
+                 "logits, top-10, renormalised, stable scatter), one moe_exl3_gate_up_down launch with moe_gather (f32 "
+                 "weighted sum, f16 out) inside its kernel (exl3c4_launch_gather)",
                  {"layers_resident": args.layers, "routing_draws": args.draws,
                   "mean_live_experts": round(float(np.mean(live)), 2)})
     out.update({
