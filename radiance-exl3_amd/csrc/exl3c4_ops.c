@@ -73,9 +73,17 @@ static int prefill_path(const Exl3c4Op* o, int64_t T) {
 #define GD_FUSE_ROWS EXL3C4_GD_FUSE_MIN_T
 #endif
 
+/* Below that, from this many rows gate_up_down forms h once a (row, 128-block) with gate_up's epilogue kernel (a wave
+ * each, all in parallel) and down stages it as given; with fewer, down's workgroups form their chunk's h while staging
+ * (one launch fewer, but every block's workgroup forms every row's h, one row after another; a build may move it). */
+#ifndef GEPI_ROWS
+#define GEPI_ROWS 2
+#endif
+
 typedef struct Carve {
     int     pf;                                   /* the prefill path */
     int     gd1;                                  /* gate_up_down as one kernel (decode path, T >= GD_FUSE_MIN_T) */
+    int     h_gepi;                               /* gate_up_down, decode path below that from GEPI_ROWS: h by k_gepi */
     int64_t row_info, plan, xr, part, h, dacc, sync, total;
     int64_t T, part_pitch, dacc_pitch, xr_pitch, h_pitch, max_chunks;
     int     split_gu, gu_lds_pitch, dn_lds_pitch;
@@ -127,8 +135,9 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
         off += ALIGN_UP(s * T * rc * 4, 256);
     }
     k->gd1 = op == EXL3C4_GU_DN && !k->pf && T >= GD_FUSE_ROWS;
+    k->h_gepi = op == EXL3C4_GU_DN && !k->pf && !k->gd1 && T >= GEPI_ROWS;
     k->h = off;
-    if ((k->pf || k->gd1) && op == EXL3C4_GU_DN) {
+    if ((k->pf || k->gd1 || k->h_gepi) && op == EXL3C4_GU_DN) {
         k->h_pitch = rc / 2;
         off += ALIGN_UP(T * k->h_pitch * 2, 256);
     }
@@ -416,7 +425,8 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
     switch (op) {
     case EXL3C4_GATE_UP: return kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_EPI_GU;
     case EXL3C4_DOWN:    return kernel == EXL3C4_K_DOWN;
-    default:             return kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_DOWN;
+    default:             return kernel == EXL3C4_K_GATE_UP || kernel == EXL3C4_K_DOWN ||
+                                (k->h_gepi && kernel == EXL3C4_K_EPI_GU);
     }
 }
 
@@ -464,6 +474,14 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
         a.nblk = (int32_t)(o->y_cols / 128);
         if ((rc = exl3c4_dev_gu(&a, stream, EV(EXL3C4_K_GATE_UP))) != 0) return rc;
         if (op == EXL3C4_GATE_UP) return exl3c4_dev_gepi(&a, stream, EV(EXL3C4_K_EPI_GU));
+        if (k.h_gepi) {                              /* h (rotated for down) into scratch, a wave a (row, block) */
+            Exl3c4Launch e = a;
+            e.h_rot = 1;
+            e.y = s + k.h;
+            e.y_pitch = k.h_pitch;
+            e.nblk = (int32_t)(max_rows(o) / 256);
+            if ((rc = exl3c4_dev_gepi(&e, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
+        }
     }
 
     /* down: its own classes, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
@@ -471,7 +489,13 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     Exl3c4Launch d;
     base_args(o, &k, s, &d);
     down_classes(o, &d);
-    if (op == EXL3C4_GU_DN) {
+    if (op == EXL3C4_GU_DN && k.h_gepi) {
+        d.row_info = (int32_t*)(s + k.row_info);     /* written by gate_up's GEMM */
+        d.x = s + k.h;                               /* h, rotated: staged as given */
+        d.x_pitch = k.h_pitch;
+        d.x_rows = (int32_t)o->T;
+        d.h_rot = 1;
+    } else if (op == EXL3C4_GU_DN) {
         d.h_from_gu = 1;
         d.row_info = (int32_t*)(s + k.row_info);     /* written by gate_up's GEMM */
         d.ksplit = k.split_gu;                       /* the gate_up partial sums it reads */
