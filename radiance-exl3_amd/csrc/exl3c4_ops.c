@@ -73,9 +73,10 @@ static int prefill_path(const Exl3c4Op* o, int64_t T) {
 #define GD_FUSE_ROWS EXL3C4_GD_FUSE_MIN_T
 #endif
 
-/* Below that, from this many rows gate_up_down forms h once a (row, 128-block) with gate_up's epilogue kernel (a wave
+/* Below that, from GEPI_ROWS rows, gate_up_down forms h once a (row, 128-block) with gate_up's epilogue kernel (a wave
  * each, all in parallel) and down stages it as given; with fewer, down's workgroups form their chunk's h while staging
- * (one launch fewer, but every block's workgroup forms every row's h, one row after another; a build may move it). */
+ * (one launch fewer, but every block's workgroup forms every row's h of its chunk, one row after another: slow when a
+ * chunk holds many rows, which the host cannot see -- n_expert counts tables, not live experts). A build may move it. */
 #ifndef GEPI_ROWS
 #define GEPI_ROWS 2
 #endif
@@ -83,7 +84,7 @@ static int prefill_path(const Exl3c4Op* o, int64_t T) {
 typedef struct Carve {
     int     pf;                                   /* the prefill path */
     int     gd1;                                  /* gate_up_down as one kernel (decode path, T >= GD_FUSE_MIN_T) */
-    int     h_gepi;                               /* gate_up_down, decode path below that from GEPI_ROWS: h by k_gepi */
+    int     h_gepi;                               /* gate_up_down, decode path below that (GEPI_ROWS): h by k_gepi */
     int64_t row_info, plan, xr, part, h, dacc, sync, total;
     int64_t T, part_pitch, dacc_pitch, xr_pitch, h_pitch, max_chunks;
     int     split_gu, gu_lds_pitch, dn_lds_pitch;
