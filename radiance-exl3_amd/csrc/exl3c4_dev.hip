@@ -717,7 +717,7 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
     __syncthreads();
     const int n = ntok_s;
     for (int j = wave; j < n; j += (int)(blockDim.x >> 6)) {
-        const int64_t t = tok_s[j];
+        const int64_t t = __builtin_amdgcn_readfirstlane(tok_s[j]);   // uniform: the slots' rows and weights in SGPRs
         const int c = b * 128 + lane;
         float acc0 = 0.f, acc1 = 0.f;
         for (int s0 = 0; s0 < a.top_k; s0 += 16) {                // 16 slots' rows and weights, then their values
