@@ -267,6 +267,8 @@ def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bit
     (82, 8, 10, 96, [(512, 256)], 0.0, True),                   # a token whose slots all drop
     (83, 5, 8, 12, [(256, 128)], 0.1, False),                   # few experts: chunks of several rows
     (84, 2, 8, 12, [(256, 128)], 0.0, False),                   # T = 16: two kernels, then the gather's own
+    (85, 1, 2, 4, [(256, 128), (512, 256)], 0.0, False),       # T = 2: the smallest h formed by the epilogue kernel
+    (86, 3, 10, 16, [(512, 256)], 0.2, False),                  # T = 30, the largest below the one-kernel form
 ])
 def test_launch_gather_gives_the_bits_of_the_launch_and_the_gather(torch_cuda, seed, n_tok, top_k, n_expert, geoms,
                                                                    drop, empty):
