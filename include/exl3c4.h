@@ -103,6 +103,11 @@ typedef struct Exl3c4Op {
  * geometry): docs/STEP0.md:142-146, kernels/exl3r4d/launch.c:263-275. Negative: the refusal the launch would give. */
 int64_t exl3c4_scratch_bytes(const Exl3c4Op* op);
 
+/* The bytes of scratch THIS launch of `op` (its T sorted rows) needs: exl3c4_launch refuses EXL3C4_E_SCRATCH below it.
+ * Never more than exl3c4_scratch_bytes(op), which is the largest of these over every row count up to the band top, so
+ * scratch sized once for the band takes every smaller batch. A query with no counterpart in the reference. */
+int64_t exl3c4_launch_scratch_bytes(const Exl3c4Op* op);
+
 /* The same from the geometry alone (no operands): the op, its classes' [rows, cols] as the op's weights are (for
  * gate_up_down: gate_up's), M tokens (a band's top), top_k and n_expert. What a plugin's scratch hook answers from
  * the parameters (docs/STEP0.md:142-146). A negative status for a geometry the op refuses. */

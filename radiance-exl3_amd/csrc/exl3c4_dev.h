@@ -32,50 +32,76 @@ extern "C" {
 #define EXL3C4_PF_W_GU 10
 #define EXL3C4_PF_W_DN 3
 
+/* One class of experts as a kernel reads it: each plane's table -- a device pointer array when its stride is 0 (the
+ * engine's form), else a stacked buffer with entry j at base + j * stride bytes -- and the class's weight geometry
+ * [rows, cols]. The op's own weight is codes / suh / svh (with suh1 and dn_suh for gate_up); for gate_up_down the class
+ * is gate_up's and dn_codes / dn_svh are down's planes, down's weight being [cols, rows / 2] with suh = dn_suh
+ * (include/exl3_abi.h:751-800). */
+typedef struct Exl3c4DevClass {
+    const void* codes;
+    const void* suh;
+    const void* suh1;
+    const void* svh;
+    const void* dn_suh;
+    const void* dn_codes;
+    const void* dn_svh;
+    int32_t     codes_s, suh_s, suh1_s, svh_s, dn_suh_s, dn_codes_s, dn_svh_s;   /* entry strides (bytes) */
+    int32_t     rows, cols;
+} Exl3c4DevClass;
+
+/* The argument block every op kernel takes by value. The radiance engine dispatches a kernel only if its argument
+ * segment -- these bytes plus any hidden argument HIP appends for a kernel that reads one (blockDim, gridDim, ...) --
+ * fits its 768-byte slot (kernels/exl3r4d/exl3r4d_dev.h:5-6, tests/gpu/kernarg_check.sh): this block is 632 bytes
+ * (EXL3C4_KERNARG_BYTES, checked at compile time) and no kernel that takes it reads a hidden argument. Hence the
+ * 32-bit pitches and strides (the host refuses larger ones) and one class record serving both GEMMs of gate_up_down. */
+#define EXL3C4_KERNARG_LIMIT 768
 typedef struct Exl3c4Launch {
-    Exl3c4Class    cls[4];        /* the GEMM's weight classes (gate_up's, or down's); prep: the scale source */
-    Exl3c4Class    gcls[4];       /* down in gate_up_down: gate_up's classes (svh, dn_suh, its partial sums) */
+    Exl3c4DevClass cls[4];        /* the op's classes: class c holds experts e % n_class == c at entry e / n_class */
     const void*    x;             /* the input: token rows, or sorted rows (a_rot gate_up; down) */
-    int64_t        x_pitch;
     void*          y;             /* the op's output */
-    int64_t        y_pitch;
     float*         part;          /* gate_up's split-K partial sums [ksplit][T][part_pitch] */
-    int64_t        part_pitch, part_split;
     float*         dacc;          /* down's raw accumulations [T][dacc_pitch] */
-    int64_t        dacc_pitch;
     int32_t*       row_info;      /* [T][2]: the row's owner expert (-1: none), the chunk's rows where one starts */
     const int32_t* sorted;
     const int32_t* off;
-    int32_t        x_dtype, x_rows, x_cols_max;
-    int32_t        T, n_expert, top_k, n_class;
-    int32_t        bits, codebook;
-    int32_t        h_rot;         /* gate_up: rotate h for down; down: the input is already rotated */
-    int32_t        a_rot;         /* gate_up: the input is already rotated (sorted rows [T][2 C]) */
-    int32_t        h_from_gu;     /* down: stage h from gate_up's partial sums (gate_up_down) */
-    int32_t        ksplit, ksplit_log2;
-    int32_t        n_grp;         /* gate_up: groups of four strips a row (the widest class's rows / 128) */
-    int32_t        nblk;          /* epilogue / down: 128-column output blocks a row */
-    int32_t        lds_pitch;     /* halves a staged input row in LDS */
-    int32_t        y_cols;
     int32_t*       plan;          /* prefill: [0] chunk count, then int4 {expert, row0, rows, 0} per chunk */
-    int32_t        max_chunks;
-    int32_t        blk_per_wave;  /* gate_up's epilogue: 128-blocks of a row one wave takes */
-    int32_t        lds_pitch_gu;  /* gate_up_down in one launch: gate_up's staged row pitch (lds_pitch is down's) */
     int32_t*       sync;          /* gate_up_down in one launch: a status word, then row i's counter at (i + 1) * SYNC_STRIDE */
     uint16_t*      hbuf;          /* gate_up_down in one launch: h (rotated, f16) of every chunk's rows [T][hbuf_pitch] */
-    int64_t        hbuf_pitch;
-    int32_t        keep_sums;     /* prefill: also leave the GEMMs' f32 sums in part / dacc (a checker's view) */
-    int32_t        tail_from;     /* prefill GEMMs: nonzero asks for workgroups that zero the rows no run holds after
-                                     the GEMM's (the launcher sets where they start) */
     /* gate_up_down in one launch with moe_gather behind it (g_out non-null): out[t] = f16(sum over the token's slots
      * of expert_w x y[row_of]); token t's counter of 128-block b at g_ctr[t * SYNC_STRIDE + b] (zero, left zero) */
     const float*   g_w;
     const int32_t* g_row_of;
     uint16_t*      g_out;
-    int64_t        g_out_pitch;
-    int32_t        g_ntok;
     int32_t*       g_ctr;
+    int32_t*       fail;          /* gate_up_down in one launch: also set to 1 when a wait gives up (host-visible), or null */
+    int32_t        x_pitch, y_pitch, part_pitch, dacc_pitch, hbuf_pitch, g_out_pitch;   /* elements */
+    int32_t        x_dtype, x_rows, x_cols_max;
+    int32_t        T, n_expert, top_k, n_class;
+    int32_t        bits, codebook;
+    int32_t        h_rot;         /* gate_up: rotate h for down; down: the input is already rotated */
+    int32_t        a_rot;         /* gate_up: the input is already rotated (sorted rows [T][2 C]) */
+    int32_t        h_from_gu;     /* down: stage h from gate_up's partial sums (gate_up_down); k_rot: halves a row */
+    int32_t        dn_gd;         /* down's weight is gate_up_down's (dn_codes / dn_svh / dn_suh of gate_up's class) */
+    int32_t        ksplit, ksplit_log2;
+    int32_t        n_grp;         /* gate_up: groups of four strips a row (the widest class's rows / 128) */
+    int32_t        nblk;          /* epilogue / down: 128-column output blocks a row */
+    int32_t        lds_pitch;     /* halves a staged input row in LDS */
+    int32_t        lds_pitch_gu;  /* gate_up_down in one launch: gate_up's staged row pitch (lds_pitch is down's) */
+    int32_t        y_cols;
+    int32_t        max_chunks;
+    int32_t        blk_per_wave;  /* gate_up's epilogue: 128-blocks of a row one wave takes */
+    int32_t        keep_sums;     /* prefill: also leave the GEMMs' f32 sums in part / dacc (a checker's view) */
+    int32_t        tail_from;     /* prefill GEMMs: nonzero asks for workgroups that zero the rows no run holds after
+                                     the GEMM's (the launcher sets where they start) */
+    int32_t        g_ntok;
 } Exl3c4Launch;
+#define EXL3C4_KERNARG_BYTES 632
+
+/* exl3c4_launch_ctr with a host-visible flag (`fail`, pinned host memory the device can write, or null) that the
+ * single gate_up_down kernel sets to 1 when a wait gives up: what the plugin rows' instances hand over, so that a
+ * later launch can report the failure without a synchronisation. Internal to the library. */
+__attribute__((visibility("hidden"))) int exl3c4_launch_inst(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes,
+                                                             void* stream, void* ctr, int64_t ctr_bytes, int32_t* fail);
 
 /* Each returns 0 or EXL3C4_E_DEVICE (a launch error). None allocates or synchronises. ev0 / ev1: hipEvent_t the
  * dispatch itself stamps at its start and end (hipExtLaunchKernelGGL), or null for a plain launch. */

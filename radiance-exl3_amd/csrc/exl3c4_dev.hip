@@ -32,6 +32,9 @@
 
 #include "exl3c4_dev.h"
 
+static_assert(sizeof(Exl3c4Launch) == EXL3C4_KERNARG_BYTES && EXL3C4_KERNARG_BYTES <= EXL3C4_KERNARG_LIMIT,
+              "the op kernels' argument block must fit the engine's kernel-argument slot");
+
 namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -46,8 +49,8 @@ constexpr float kHadScale = 0.08838834764831844055f;   // (float)(1/sqrt(128)), 
 
 // ------------------------------------------------------------------------------------------------ scalar helpers
 
-__device__ __forceinline__ const void* tab_entry(const void* base, int64_t stride, int64_t j) {
-    return stride ? (const void*)((const char*)base + j * stride) : ((const void* const*)base)[j];
+__device__ __forceinline__ const void* tab_entry(const void* base, int32_t stride, int64_t j) {
+    return stride ? (const void*)((const char*)base + j * (int64_t)stride) : ((const void* const*)base)[j];
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -362,7 +365,7 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
     if (e < 0) return;
     const int c = class_of(a, e);
     const int64_t jx = entry_of(a, e);
-    const Exl3c4Class& K = a.cls[c];
+    const Exl3c4DevClass& K = a.cls[c];
     const int C = K.cols;
     if (b * 128 >= C) return;
     uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + (int64_t)m * C + b * 128;
@@ -375,7 +378,7 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
     int64_t src = tok / a.top_k;
     src = src < a.x_rows ? src : a.x_rows - 1;
     const void* x = (const uint16_t*)a.x + src * a.x_pitch + b * 128;
-    const void* s = m ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    const void* s = m ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx);
     const uint16_t x0 = ldg16(x, lane), x1 = ldg16(x, 64 + lane);
     const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
     const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
@@ -406,7 +409,7 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
     const __attribute__((address_space(1))) float* p =
         (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
     const int S = a.ksplit;
-    const int64_t st = a.part_split;
+    const int64_t st = (int64_t)a.T * a.part_pitch;               // one split's sums: [T][part_pitch]
     if (S < 4) {                                                  // 1 or 2
         float v[4][2];
 #pragma unroll
@@ -464,13 +467,13 @@ __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0
 // values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
 // 187-212).
 template <bool COH>
-__device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4Class& K, int64_t i, int b, int64_t jx,
-                                              int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
-    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
+__device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4DevClass& K, int64_t i, int b,
+                                              int64_t jx, int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
+    const void* svh = tab_entry(K.svh, K.svh_s, jx);
     const int n0 = b * 128 + lane, n1 = n0 + 64;
     const int width = K.rows / 2;
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
-    const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
     const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
     const int col[4] = { n0, n1, width + n0, width + n1 };
     float acc[4];
@@ -537,7 +540,7 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r
 // part[split][row][col]; their consumer adds the splits in a fixed order, so the bits do not depend on scheduling.
 // Unit u = group u >> ksplit_log2, split u & (S - 1) of row i; kp: halves a staged row. Returns the chunk's rows (0 when
 // row i starts none) and the row's owner. In its own kernel (k_gu) unit 0 of each row records the row's owner and chunk rows in row_info
-// for the kernels that follow; inside gate_up_down's single launch (FUSED) the classes are gcls.
+// for the kernels that follow; inside gate_up_down's single launch (FUSED) nothing follows, so it records nothing.
 struct GuRows { int nrows, e; };
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, int kp, unsigned char* lds) {
@@ -553,7 +556,7 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     if (nrows == 0) return GuRows{ 0, w.e };
     const int c = class_of(a, w.e);
     const int64_t jx = entry_of(a, w.e);
-    const Exl3c4Class& K = FUSED ? a.gcls[c] : a.cls[c];
+    const Exl3c4DevClass& K = a.cls[c];
     const int N = K.rows, KC = K.cols;
     if (grp * 128 >= N) return GuRows{ nrows, w.e };
     const int strip = grp * 4 + wave;
@@ -561,13 +564,13 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     const int nb = KC / 128, per = (nb + S - 1) / S;
     const int b0 = min(nb, split * per), b1 = min(nb, b0 + per);
     const int ksn = 2 * (b1 - b0);
-    const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_stride, jx) +
+    const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_s, jx) +
                       ((int64_t)strip * (KC / EXL3C4_KSTEP) + 2 * b0) * 64 * BITS + lane * BITS;
     CodeRing<BITS> ring;
     prime<BITS>(rec, ksn, ring);                                  // its first steps' words fly during the staging
 
     uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
-    const void* sv = up ? tab_entry(K.suh1, K.suh1_stride, jx) : tab_entry(K.suh, K.suh_stride, jx);
+    const void* sv = up ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx);
     for (int q = 0; q < nrows; ++q) {
         const int64_t r = i + q;
         const int tok = a.a_rot ? 0 : a.sorted[r];
@@ -597,7 +600,7 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     // D lane l: column l % 16 (c' = 2 s + t -> weight row 32 nb + 16 t + s, + 8 for acc1), rows 4 (l / 16) + 0..3
     const int cc = lane & 15, rg = lane >> 4;
     const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
-    float* pp = a.part + (int64_t)split * a.part_split;
+    float* pp = a.part + (int64_t)split * a.T * a.part_pitch;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int tok = rg * 4 + q;
@@ -646,7 +649,8 @@ __device__ __forceinline__ int32_t* row_counter(const Exl3c4Launch& a, int i) {
 // A down unit of gate_up_down's single launch waits here until its chunk's h is stored: row i's counter reaches
 // n_grp x ksplit + 1 (one count per gate_up unit of row i once its sums are stored, one more once the last of them has
 // formed h). The wait gives up after EXL3C4_WAIT_TICKS of the 100 MHz clock, or soon after another workgroup gave up,
-// and sets bit 0 of the status word sync[0] (the output is then void; the launch still ends).
+// and sets bit 0 of the status word sync[0] -- and *fail, a flag the host can read without a synchronisation, when
+// the launch has one (the plugin rows' instances) -- the output is then void; the launch still ends.
 #define EXL3C4_WAIT_TICKS 50000000ull
 __device__ __forceinline__ void wait_gate_up(const Exl3c4Launch& a, int i) {
     if (threadIdx.x == 0) {
@@ -658,6 +662,7 @@ __device__ __forceinline__ void wait_gate_up(const Exl3c4Launch& a, int i) {
             if ((n & 15) == 0 && ((__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1) ||
                                   __builtin_amdgcn_s_memrealtime() - t0 > EXL3C4_WAIT_TICKS)) {
                 __hip_atomic_fetch_or(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (a.fail) __hip_atomic_store(a.fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 break;
             }
         }
@@ -706,7 +711,10 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
                 const int old = __hip_atomic_fetch_add(a.g_ctr + (int64_t)t * EXL3C4_SYNC_STRIDE + b, 1,
                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 int need = 0;                                     // read while the count is in flight
-                for (int s = 0; s < a.top_k; ++s) need += a.g_row_of[(int64_t)t * a.top_k + s] >= 0;
+                for (int s = 0; s < a.top_k; ++s) {              // a slot has a row when 0 <= row < T, as the
+                    const int r = a.g_row_of[(int64_t)t * a.top_k + s];   // sum and gather_empty read it
+                    need += (r >= 0 && r < a.T) ? 1 : 0;
+                }
                 last = old == need - 1;
             }
         }
@@ -716,7 +724,7 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
     }
     __syncthreads();
     const int n = ntok_s;
-    for (int j = wave; j < n; j += (int)(blockDim.x >> 6)) {
+    for (int j = wave; j < n; j += 4) {                            // k_gd: 4 waves a workgroup
         const int64_t t = __builtin_amdgcn_readfirstlane(tok_s[j]);   // uniform: the slots' rows and weights in SGPRs
         const int c = b * 128 + lane;
         float acc0 = 0.f, acc1 = 0.f;
@@ -757,13 +765,21 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
 // takes token 4 z + w.
 __device__ __forceinline__ void gather_empty(const Exl3c4Launch& a, int z) {
     const int lane = threadIdx.x & 63;
-    const int64_t t = (int64_t)z * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int64_t t = (int64_t)z * 4 + (threadIdx.x >> 6);        // k_gd: 4 waves a workgroup
     if (t >= a.g_ntok) return;
     for (int s = 0; s < a.top_k; ++s) {
         const int r = a.g_row_of[t * a.top_k + s];
         if (r >= 0 && r < a.T) return;
     }
     for (int c = lane; c < a.y_cols; c += 64) a.g_out[t * a.g_out_pitch + c] = 0;
+}
+
+// down's weight as a kernel reads it: the op's own (the down op), or gate_up_down's -- dn_codes / dn_svh of gate_up's
+// class, [cols, rows / 2], with suh = dn_suh (include/exl3_abi.h:751-800)
+struct DnW { const void *codes, *svh, *suh; int32_t codes_s, svh_s, suh_s; int rows, cols; };
+__device__ __forceinline__ DnW dn_weight(bool gd, const Exl3c4DevClass& K) {
+    if (gd) return DnW{ K.dn_codes, K.dn_svh, K.dn_suh, K.dn_codes_s, K.dn_svh_s, K.dn_suh_s, K.cols, K.rows / 2 };
+    return DnW{ K.codes, K.svh, K.suh, K.codes_s, K.svh_s, K.suh_s, K.rows, K.cols };
 }
 
 template <int BITS, int CB, bool FUSED>
@@ -789,7 +805,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     if (nrows == 0) return;
     const int c = class_of(a, e);
     const int64_t jx = entry_of(a, e);
-    const Exl3c4Class& D = a.cls[c];
+    const DnW D = dn_weight(FUSED || a.dn_gd, a.cls[c]);
     const int N = D.rows, KC = D.cols;
     if (b * 128 >= N) {                                           // a narrower class's tail
         for (int q = wave; q < nrows; q += 4)
@@ -804,12 +820,12 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     // this wave's strip of the block, all of k; its first codes are in flight while the rows are staged
     const int strip = 4 * b + wave;
     const int ksteps = KC / EXL3C4_KSTEP;
-    const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    const gu32p rec = (gu32p)tab_entry(D.codes, D.codes_s, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     CodeRing<BITS> ring;
     prime<BITS>(rec, ksteps, ring);
-    const void* svh = tab_entry(D.svh, D.svh_stride, jx);
+    const void* svh = tab_entry(D.svh, D.svh_s, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
-    const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_stride, jx) : nullptr;
+    const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_s, jx) : nullptr;
     if (FUSED) {
         wait_gate_up(a, i);
         // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the
@@ -834,7 +850,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
                 v0 = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 v1 = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else if (a.h_from_gu) {
-                if (a.sorted[r] >= 0) gate_up_block<false>(a, a.gcls[c], r, hb, jx, 1, lane, v0, v1);
+                if (a.sorted[r] >= 0) gate_up_block<false>(a, a.cls[c], r, hb, jx, 1, lane, v0, v1);
             } else {
                 const void* xs = (const uint16_t*)a.x + r * a.x_pitch + hb * 128;
                 const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
@@ -897,7 +913,7 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int c = class_of(a, g.e);
     const int64_t jx = entry_of(a, g.e);
-    const Exl3c4Class& G = a.gcls[c];
+    const Exl3c4DevClass& G = a.cls[c];
     const int nhb = G.rows / 256;                                  // h's 128-blocks: (rows / 2) / 128
     for (int t = wave; t < g.nrows * nhb; t += 4) {
         const int q = t / nhb, hb = t - q * nhb;
@@ -1128,7 +1144,7 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int e = owner_wave(a.off, a.n_expert, i, lane);       // the plan (beside) writes row_info later
     const int tok = a.sorted[i];
     if (e < 0) return;
-    const Exl3c4Class& K = a.cls[class_of(a, e)];
+    const Exl3c4DevClass& K = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
     const int C = K.cols;
     uint16_t* out = (uint16_t*)a.y + (int64_t)i * a.y_pitch;
@@ -1145,8 +1161,8 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     int64_t src = halves == 2 ? tok / a.top_k : i;
     src = src < a.x_rows ? src : a.x_rows - 1;
     const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch;
-    const uint16_t* s0 = (const uint16_t*)tab_entry(K.suh, K.suh_stride, jx);
-    const uint16_t* s1 = halves == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_stride, jx) : s0;
+    const uint16_t* s0 = (const uint16_t*)tab_entry(K.suh, K.suh_s, jx);
+    const uint16_t* s1 = halves == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_s, jx) : s0;
     const bool xw = (((uintptr_t)a.x | (uintptr_t)(a.x_pitch * 2)) & 15) == 0;
     const bool sw = (((uintptr_t)s0 | (uintptr_t)s1) & 15) == 0;
     const bool bf = halves == 2 && a.x_dtype == EXL3C4_BF16;
@@ -1195,10 +1211,11 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
 }
 
 // Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows): wave w of
-// workgroup z takes row z * waves + w: the workgroups from a.tail_from of the last GEMM's launch.
-__device__ __forceinline__ void zero_dead_rows(const Exl3c4Launch& a, int z) {
-    const int nw = (int)(blockDim.x >> 6), lane = threadIdx.x & 63;
-    const int64_t i = (int64_t)z * nw + (threadIdx.x >> 6);
+// workgroup z takes row z * NW + w (NW: the kernel's waves a workgroup): the workgroups from a.tail_from of the last
+// GEMM's launch.
+template <int NW> __device__ __forceinline__ void zero_dead_rows(const Exl3c4Launch& a, int z) {
+    const int lane = threadIdx.x & 63;
+    const int64_t i = (int64_t)z * NW + (threadIdx.x >> 6);
     if (i >= a.T || a.row_info[2 * i] >= 0) return;
     uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
     for (int b = 0; b < a.nblk; ++b) {
@@ -1281,17 +1298,18 @@ __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32
 // waves, two staged inputs (columns k and half_off + k), thread t staging half t / 256 and wave w reading half w / 4.
 // NT: the chunk's 16-row tiles (ceil(nrows / 16)), a template argument so that the loop holds no branch on it.
 // Accumulations: acc[row tile][strip half].
+// The weight: entry jx of the codes table (codes, codes_s) of k = KC columns.
 template <int BITS, int CB, int NH, int NT>
-__device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
+__device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, int KC, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
                                         int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
     const int lane = threadIdx.x & 63;
-    const int KC = W.cols, nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
+    const int nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
     const int kp = 128 + 8;
     const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
     const int scol = col_off + sh * half_off;                     // this thread's staged input column
     auto bufp = [&](int b, int h) { return lds + (b * NH + h) * 64 * kp; };
-    const gu32p rec = (gu32p)tab_entry(W.codes, W.codes_stride, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
+    const gu32p rec = (gu32p)tab_entry(codes, codes_s, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     // the codes of the steps ahead: dA even steps, dB odd; each refill 2 steps ahead of the step it serves (clamped:
     // past the stream a harmless reload of the last step, unconditional so that the waits count exactly)
     uint32_t dA[BITS], dB[BITS];
@@ -1323,15 +1341,17 @@ __device__ __forceinline__ void pf_gemm_nt(const Exl3c4Launch& a, const Exl3c4Cl
 }
 
 template <int BITS, int CB, int NH>
-__device__ __forceinline__ void pf_gemm(const Exl3c4Launch& a, const Exl3c4Class& W, int64_t jx, int strip,
+__device__ __forceinline__ void pf_gemm(const void* codes, int32_t codes_s, int KC, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
                                         int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
+#define EXL3C4_PF_ARGS codes, codes_s, KC, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc
     switch ((nrows + 15) >> 4) {
-    case 1: pf_gemm_nt<BITS, CB, NH, 1>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
-    case 2: pf_gemm_nt<BITS, CB, NH, 2>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
-    case 3: pf_gemm_nt<BITS, CB, NH, 3>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
-    default: pf_gemm_nt<BITS, CB, NH, 4>(a, W, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc); break;
+    case 1: pf_gemm_nt<BITS, CB, NH, 1>(EXL3C4_PF_ARGS); break;
+    case 2: pf_gemm_nt<BITS, CB, NH, 2>(EXL3C4_PF_ARGS); break;
+    case 3: pf_gemm_nt<BITS, CB, NH, 3>(EXL3C4_PF_ARGS); break;
+    default: pf_gemm_nt<BITS, CB, NH, 4>(EXL3C4_PF_ARGS); break;
     }
+#undef EXL3C4_PF_ARGS
 }
 
 // gate_up's prefill GEMM with its epilogue: one workgroup of 8 waves per (chunk, h-block hb): waves 0..3 the 4 gate
@@ -1345,7 +1365,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
     constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
     if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // gate_up alone: the rows no run holds
-        zero_dead_rows(a, (int)blockIdx.x - a.tail_from);
+        zero_dead_rows<8>(a, (int)blockIdx.x - a.tail_from);
         return;
     }
     int hb, chunk;
@@ -1354,7 +1374,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
               nrows = __builtin_amdgcn_readfirstlane(ent.z);      // one chunk a workgroup: uniform
-    const Exl3c4Class& K = a.cls[class_of(a, e)];
+    const Exl3c4DevClass& K = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
     const int N = K.rows, KC = K.cols, width = N / 2;
     if (hb * 128 >= width) {                                      // a narrower class: its rows' block past its width
@@ -1371,7 +1391,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-    pf_gemm<BITS, CB, 2>(a, K, jx, strip, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, KC, lds, acc);
+    pf_gemm<BITS, CB, 2>(K.codes, K.codes_s, KC, jx, strip, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, KC, lds,
+                         acc);
     const int cc = lane & 15, rg = lane >> 4;
     const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
     const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
@@ -1391,8 +1412,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             }
         }
     __syncthreads();
-    const void* svh = tab_entry(K.svh, K.svh_stride, jx);
-    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_stride, jx) : nullptr;
+    const void* svh = tab_entry(K.svh, K.svh_s, jx);
+    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
     const int n0 = hb * 128 + lane, n1 = n0 + 64;
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
     const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
@@ -1417,7 +1438,7 @@ template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
     if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // the rows no run holds
-        zero_dead_rows(a, (int)blockIdx.x - a.tail_from);
+        zero_dead_rows<4>(a, (int)blockIdx.x - a.tail_from);
         return;
     }
     int b, chunk;
@@ -1426,7 +1447,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
               nrows = __builtin_amdgcn_readfirstlane(ent.z);      // one chunk a workgroup: uniform
-    const Exl3c4Class& D = a.cls[class_of(a, e)];
+    const DnW D = dn_weight(a.dn_gd, a.cls[class_of(a, e)]);
     const int64_t jx = entry_of(a, e);
     const int N = D.rows;
     if (b * 128 >= N) {                                           // a narrower class's tail
@@ -1441,9 +1462,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float4_t acc[4][2];
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-    pf_gemm<BITS, CB, 1>(a, D, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0, lds, acc);
+    pf_gemm<BITS, CB, 1>(D.codes, D.codes_s, D.cols, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0,
+                         lds, acc);
 
-    const void* svh = tab_entry(D.svh, D.svh_stride, jx);
+    const void* svh = tab_entry(D.svh, D.svh_s, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
     float* acc_l = (float*)lds;                                   // [16][128], one row tile at a time
     const int cc = lane & 15, rg = lane >> 4;

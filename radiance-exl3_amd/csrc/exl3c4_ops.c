@@ -8,7 +8,8 @@
  *   EXL3C4_E_DTYPE    K outside 2..8, an unknown codebook, an activation of a dtype the op does not read
  *   EXL3C4_E_SHAPE    extents the format cannot hold (every K % 128, gate_up N % 256, down N % 128), a
  *                     non-positive count, an output not exactly the op's width, an input narrower than it reads
- *   EXL3C4_E_STRIDE   a row pitch below its width
+ *   EXL3C4_E_STRIDE   a row pitch below its width; a table's entry stride below its entry; a pitch or a stride past
+ *                     2^31 - 1 (the kernels' argument block holds them in 32 bits)
  *   EXL3C4_E_ALIGN    a sorted-row input the 16-byte activation loads cannot take; a misaligned table
  *   EXL3C4_E_SCRATCH  less scratch than exl3c4_scratch_bytes asks for
  * The routing VALUES live in device memory and are not read here (that would be a synchronisation): the kernels
@@ -20,6 +21,9 @@
 #include "exl3c4_dev.h"
 
 #define ALIGN_UP(x, a) (((x) + (a) - 1) / (a) * (a))
+
+_Static_assert(sizeof(Exl3c4Launch) == EXL3C4_KERNARG_BYTES && EXL3C4_KERNARG_BYTES <= EXL3C4_KERNARG_LIMIT,
+               "the op kernels' argument block must fit the engine's kernel-argument slot");
 
 static int is_gate_up(int op) { return op == EXL3C4_GATE_UP || op == EXL3C4_PREP_GU || op == EXL3C4_GU_DN; }
 
@@ -175,6 +179,15 @@ static int class_ok(const Exl3c4Op* o, const Exl3c4Class* c, int gate_up_geom, i
     if ((c->suh_stride | c->suh1_stride | c->svh_stride | c->dn_suh_stride) & 1) return EXL3C4_E_ALIGN;
     if (need_codes && c->codes_stride && c->codes_stride < exl3c4_record_bytes(c->rows, c->cols, o->bits))
         return EXL3C4_E_STRIDE;
+    /* a stacked scale table's entries hold the whole vector: suh / suh1 [cols], svh [rows], dn_suh [rows / 2] */
+    if ((c->suh_stride && c->suh_stride < 2 * (int64_t)c->cols) ||
+        (need_suh1 && c->suh1_stride && c->suh1_stride < 2 * (int64_t)c->cols) ||
+        (need_codes && c->svh_stride && c->svh_stride < 2 * (int64_t)c->rows) ||
+        (need_dn_suh && c->dn_suh_stride && c->dn_suh_stride < (int64_t)c->rows))
+        return EXL3C4_E_STRIDE;
+    if (c->codes_stride > INT32_MAX || c->suh_stride > INT32_MAX || c->suh1_stride > INT32_MAX ||
+        c->svh_stride > INT32_MAX || c->dn_suh_stride > INT32_MAX)
+        return EXL3C4_E_STRIDE;
     return EXL3C4_OK;
 }
 
@@ -201,6 +214,11 @@ static int check(const Exl3c4Op* o) {
             if (d->codes_stride < 0 || d->svh_stride < 0) return EXL3C4_E_STRIDE;
             if (d->codes_stride && (d->codes_stride % 4 || (uintptr_t)d->codes % 4)) return EXL3C4_E_ALIGN;
             if (d->svh_stride & 1) return EXL3C4_E_ALIGN;
+            /* down's [cols, rows / 2] weight: a stacked entry holds its record, svh [cols] */
+            if (d->codes_stride && d->codes_stride < exl3c4_record_bytes(d->rows, d->cols, o->bits))
+                return EXL3C4_E_STRIDE;
+            if (d->svh_stride && d->svh_stride < 2 * (int64_t)d->rows) return EXL3C4_E_STRIDE;
+            if (d->codes_stride > INT32_MAX || d->svh_stride > INT32_MAX) return EXL3C4_E_STRIDE;
         }
     }
     /* down stages a chunk's 16 input rows in LDS: at most 1536 columns (49 KiB) */
@@ -214,7 +232,7 @@ static int check(const Exl3c4Op* o) {
     const int64_t xc = max_cols(o), rc = max_rows(o);
     const int64_t need_x = op == EXL3C4_GATE_UP && o->a_rot ? 2 * xc : xc;
     if (o->x_cols < need_x) return EXL3C4_E_SHAPE;
-    if (o->x_pitch < o->x_cols) return EXL3C4_E_STRIDE;
+    if (o->x_pitch < o->x_cols || o->x_pitch > INT32_MAX) return EXL3C4_E_STRIDE;
     if (!token_rows && o->x_rows < o->T) return EXL3C4_E_SHAPE;
     if (token_rows && o->x_rows < 1 && o->T > 0) return EXL3C4_E_SHAPE;
     const int gemm_reads_x = (op == EXL3C4_GATE_UP && o->a_rot) || (op == EXL3C4_DOWN && o->h_rot);
@@ -223,9 +241,23 @@ static int check(const Exl3c4Op* o) {
     /* the output: exactly the op's width */
     const int64_t want = op == EXL3C4_PREP_GU ? 2 * xc : op == EXL3C4_GATE_UP ? rc / 2 : op == EXL3C4_GU_DN ? xc : rc;
     if (o->y_cols != want) return EXL3C4_E_SHAPE;
-    if (o->y_pitch < o->y_cols) return EXL3C4_E_STRIDE;
+    if (o->y_pitch < o->y_cols || o->y_pitch > INT32_MAX) return EXL3C4_E_STRIDE;
     if ((uintptr_t)o->y % 2) return EXL3C4_E_ALIGN;
     return EXL3C4_OK;
+}
+
+/* The scratch a launch of any T' in [1, Ttop] sorted rows needs: the largest carve over them. The carve is not
+ * monotone in T: the decode path's split-K count grows as T shrinks (so its partial sums s T' N can grow), and the
+ * prefill path's regions replace the decode path's at its threshold. A caller that sizes scratch once, at the band top
+ * (docs/STEP0.md:142-146), must be able to launch every smaller batch in it. */
+static int64_t carve_max(const Exl3c4Op* o, int64_t Ttop) {
+    int64_t m = 0;
+    Carve k;
+    for (int64_t t = 1; t <= Ttop; ++t) {
+        carve(o, t, &k);
+        if (k.total > m) m = k.total;
+    }
+    return m;
 }
 
 int64_t exl3c4_scratch_bytes(const Exl3c4Op* o) {
@@ -233,10 +265,18 @@ int64_t exl3c4_scratch_bytes(const Exl3c4Op* o) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     q = *o;
-    q.T = o->M * o->top_k;
+    q.T = o->M * o->top_k > o->T ? o->M * o->top_k : o->T;
+    if (q.x_rows < q.T) q.x_rows = q.T;   /* sized from the geometry: a sorted-row input as long as the band top */
     if ((rc = check(&q)) != EXL3C4_OK) return rc;
+    return carve_max(&q, q.T);
+}
+
+int64_t exl3c4_launch_scratch_bytes(const Exl3c4Op* o) {
+    int rc;
+    if (!o) return EXL3C4_E_INVAL;
+    if ((rc = check(o)) != EXL3C4_OK) return rc;
     Carve k;
-    carve(&q, q.T > o->T ? q.T : o->T, &k);
+    carve(o, o->T, &k);
     return k.total;
 }
 
@@ -260,19 +300,46 @@ int64_t exl3c4_scratch_bytes_geom(int32_t op, int32_t n_class, const int32_t* ro
         q.cls[c].rows = rows[c];
         q.cls[c].cols = cols[c];
     }
-    carve(&q, M * top_k, &k);
-    return k.total;
+    (void)k;
+    return carve_max(&q, M * top_k);
 }
 
 /* ------------------------------------------------------------------ the launch */
 
+/* The classes as the kernels read them: every plane of class c of the op (gate_up_down: gate_up's, and down's codes
+ * and svh as dn_codes / dn_svh). check() has bounded every stride to 32 bits. */
+static void dev_classes(const Exl3c4Op* o, Exl3c4Launch* a) {
+    for (int c = 0; c < o->n_class; ++c) {
+        const Exl3c4Class* g = &o->cls[c];
+        Exl3c4DevClass* d = &a->cls[c];
+        d->codes = g->codes;
+        d->suh = g->suh;
+        d->suh1 = g->suh1;
+        d->svh = g->svh;
+        d->dn_suh = g->dn_suh;
+        d->codes_s = (int32_t)g->codes_stride;
+        d->suh_s = (int32_t)g->suh_stride;
+        d->suh1_s = (int32_t)g->suh1_stride;
+        d->svh_s = (int32_t)g->svh_stride;
+        d->dn_suh_s = (int32_t)g->dn_suh_stride;
+        d->rows = g->rows;
+        d->cols = g->cols;
+        if (o->op == EXL3C4_GU_DN) {
+            d->dn_codes = o->dn[c].codes;
+            d->dn_svh = o->dn[c].svh;
+            d->dn_codes_s = (int32_t)o->dn[c].codes_stride;
+            d->dn_svh_s = (int32_t)o->dn[c].svh_stride;
+        }
+    }
+}
+
 static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* a) {
     memset(a, 0, sizeof *a);
+    dev_classes(o, a);
     a->sorted = o->sorted_tok;
     a->off = o->expert_offset;
     a->part = (float*)(s + k->part);
-    a->part_pitch = k->part_pitch;
-    a->part_split = k->T * k->part_pitch;
+    a->part_pitch = (int32_t)k->part_pitch;
     a->T = (int32_t)o->T;
     a->n_expert = (int32_t)o->n_expert;
     a->top_k = (int32_t)o->top_k;
@@ -280,41 +347,39 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->bits = o->bits;
     a->codebook = o->codebook;
     a->x = o->x;
-    a->x_pitch = o->x_pitch;
+    a->x_pitch = (int32_t)o->x_pitch;
     a->x_dtype = o->x_dtype;
     a->x_rows = (int32_t)o->x_rows;
     a->x_cols_max = (int32_t)max_cols(o);
     a->y = o->y;
-    a->y_pitch = o->y_pitch;
+    a->y_pitch = (int32_t)o->y_pitch;
     a->y_cols = (int32_t)o->y_cols;
     a->blk_per_wave = 1;
 }
 
 /* How a launch runs: the events of a timed launch go to exactly one kernel of the sequence; keep_sums has the
- * prefill GEMMs also write their f32 sums to scratch (exl3c4_launch_checked). */
-typedef struct Timed { int kernel; void *ev0, *ev1; int keep_sums; } Timed;
+ * prefill GEMMs also write their f32 sums to scratch (exl3c4_launch_checked); ctr: gate_up_down's counter block from
+ * the caller (exl3c4_launch_ctr), or null; gx: moe_gather riding in gate_up_down's single kernel
+ * (exl3c4_launch_gather), or null; fail: a host-visible flag the single kernel sets when a wait gives up, or null. */
+typedef struct {
+    const float*   w;
+    const int32_t* row_of;
+    void*          out;
+    int64_t        out_pitch;
+} Gather;
+typedef struct Ctx {
+    int           kernel;
+    void *        ev0, *ev1;
+    int           keep_sums;
+    int32_t*      ctr;
+    const Gather* gx;
+    int32_t*      fail;
+} Ctx;
 #define EV(k) (t->kernel == (k) ? t->ev0 : NULL), (t->kernel == (k) ? t->ev1 : NULL)
-
-/* down's classes: its own, or gate_up_down's [cols, rows / 2] over h with suh = gate_up's dn_suh
- * (include/exl3_abi.h:751-800; h crosses rotated). */
-static void down_classes(const Exl3c4Op* o, Exl3c4Launch* d) {
-    for (int c = 0; c < o->n_class; ++c) {
-        if (o->op == EXL3C4_GU_DN) {
-            d->cls[c] = o->dn[c];
-            d->cls[c].rows = o->cls[c].cols;
-            d->cls[c].cols = o->cls[c].rows / 2;
-            d->cls[c].suh = o->cls[c].dn_suh;
-            d->cls[c].suh_stride = o->cls[c].dn_suh_stride;
-            d->gcls[c] = o->cls[c];
-        } else {
-            d->cls[c] = o->cls[c];
-        }
-    }
-}
 
 /* The prefill path: plan; the input rotation into scratch (unless the input arrives rotated); gate_up's GEMM and its
  * epilogue (into y, or into h for gate_up_down); down's GEMM with its epilogue; the rows no run holds zeroed. */
-static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t) {
+static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Ctx* t) {
     const int op = o->op;
     int rc;
     Exl3c4Launch p;
@@ -330,9 +395,8 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     int64_t din_pitch = o->x_pitch;
     if (k->xr_pitch) {                            /* the rotation, its launch's last workgroup planning beside it */
         Exl3c4Launch r = p;
-        for (int c = 0; c < o->n_class; ++c) r.cls[c] = o->cls[c];
         r.y = s + k->xr;
-        r.y_pitch = k->xr_pitch;
+        r.y_pitch = (int32_t)k->xr_pitch;
         r.h_from_gu = op == EXL3C4_DOWN ? 1 : 2;  /* halves a row */
         if ((rc = exl3c4_dev_rot(&r, stream, EV(EXL3C4_K_PREP))) != 0) return rc;
         if (op == EXL3C4_DOWN) { din = s + k->xr; din_pitch = k->xr_pitch; }
@@ -342,13 +406,12 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
     }
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a = p;
-        for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
         a.x = gin;
-        a.x_pitch = gin_pitch;
+        a.x_pitch = (int32_t)gin_pitch;
         a.ksplit = 1;
         a.n_grp = (int32_t)(max_rows(o) / 128);
         a.h_rot = op == EXL3C4_GU_DN ? 1 : o->h_rot;
-        if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
+        if (op == EXL3C4_GU_DN) { a.y = s + k->h; a.y_pitch = (int32_t)k->h_pitch; a.nblk = (int32_t)(k->h_pitch / 128); }
         else a.nblk = (int32_t)(o->y_cols / 128);
         /* the GEMM with its epilogue: h (rotated for down when h_rot) for every row a chunk holds; gate_up alone
          * also zeroes the rows no run holds, in workgroups after the GEMM's */
@@ -359,32 +422,24 @@ static int launch_prefill(const Exl3c4Op* o, const Carve* k, char* s, void* stre
         din_pitch = k->h_pitch;
     }
     Exl3c4Launch d = p;
-    down_classes(o, &d);
+    d.dn_gd = op == EXL3C4_GU_DN;                 /* gate_up_down: down's planes of gate_up's classes */
     d.x = din;
-    d.x_pitch = din_pitch;
+    d.x_pitch = (int32_t)din_pitch;
     d.nblk = (int32_t)(o->y_cols / 128);
     d.dacc = (float*)(s + k->dacc);
-    d.dacc_pitch = k->dacc_pitch;
+    d.dacc_pitch = (int32_t)k->dacc_pitch;
     d.tail_from = 1;                              /* and the rows no run holds, zeroed after the GEMM's workgroups */
     return exl3c4_dev_dn_pf(&d, stream, EV(EXL3C4_K_DOWN));
 }
 
 /* gate_up_down at decode as one kernel: the row counters and status zeroed (or the caller's zeroed block taken), then
- * k_gd (gate_up units, then down units waiting on their row's counter; the row's last down unit zeroes its counters). */
-/* moe_gather riding in gate_up_down's single kernel (exl3c4_launch_gather) */
-typedef struct {
-    const float*   w;
-    const int32_t* row_of;
-    void*          out;
-    int64_t        out_pitch;
-} Gather;
-
-static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Timed* t, int32_t* ctr,
-                      const Gather* gx) {
+ * k_gd (gate_up units, then down units waiting on their row's counter; the row's last down unit zeroes its counters),
+ * with moe_gather inside when asked (exl3c4_launch_gather). */
+static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, const Ctx* t) {
     int rc;
     Exl3c4Launch g;
     base_args(o, k, s, &g);
-    down_classes(o, &g);                          /* cls: down's; gcls: gate_up's */
+    g.dn_gd = 1;
     g.h_from_gu = 1;
     g.ksplit = k->split_gu;
     g.ksplit_log2 = log2i(k->split_gu);
@@ -393,22 +448,23 @@ static int launch_gd1(const Exl3c4Op* o, const Carve* k, char* s, void* stream, 
     g.lds_pitch = k->dn_lds_pitch;
     g.nblk = (int32_t)(o->y_cols / 128);
     g.dacc = (float*)(s + k->dacc);
-    g.dacc_pitch = k->dacc_pitch;
+    g.dacc_pitch = (int32_t)k->dacc_pitch;
     g.hbuf = (uint16_t*)(s + k->h);
-    g.hbuf_pitch = k->h_pitch;
-    if (ctr) {                                    /* the caller's counter block: zero, and left zero */
-        g.sync = ctr;
+    g.hbuf_pitch = (int32_t)k->h_pitch;
+    g.fail = t->fail;
+    if (t->ctr) {                                 /* the caller's counter block: zero, and left zero */
+        g.sync = t->ctr;
     } else {
         g.sync = (int32_t*)(s + k->sync);
         if ((rc = exl3c4_dev_fill(g.sync, (o->T + 1) * EXL3C4_SYNC_STRIDE, stream)) != 0) return rc;
     }
-    if (gx) {                                     /* only with the caller's block: the token counters follow the rows' */
-        g.g_w = gx->w;
-        g.g_row_of = gx->row_of;
-        g.g_out = (uint16_t*)gx->out;
-        g.g_out_pitch = gx->out_pitch;
+    if (t->gx) {                                  /* only with the caller's block: the token counters follow the rows' */
+        g.g_w = t->gx->w;
+        g.g_row_of = t->gx->row_of;
+        g.g_out = (uint16_t*)t->gx->out;
+        g.g_out_pitch = (int32_t)t->gx->out_pitch;
         g.g_ntok = (int32_t)o->M;
-        g.g_ctr = ctr + (o->T + 1) * EXL3C4_SYNC_STRIDE;
+        g.g_ctr = t->ctr + (o->T + 1) * EXL3C4_SYNC_STRIDE;
     }
     return exl3c4_dev_gd(&g, stream, EV(EXL3C4_K_GATE_UP_DOWN));
 }
@@ -439,8 +495,7 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
  *   gate_up_down  gate_up's GEMM, then down's, whose workgroups build h from gate_up's partial sums; from
  *                 GD_FUSE_MIN_T rows both GEMMs in one kernel (launch_gd1)
  * Prefill (launch_prefill) plans 64-row chunks of one expert first and runs one GEMM kernel a projection. */
-static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Timed* t,
-                       int32_t* ctr, const Gather* gx) {
+static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, const Ctx* t) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     if ((rc = check(o)) != EXL3C4_OK) return rc;
@@ -454,17 +509,15 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     if (op == EXL3C4_PREP_GU) {
         Exl3c4Launch f;
         base_args(o, &k, s, &f);
-        for (int c = 0; c < o->n_class; ++c) f.cls[c] = o->cls[c];
         return exl3c4_dev_prep(&f, stream, EV(EXL3C4_K_PREP));
     }
 
     if (k.pf) return launch_prefill(o, &k, s, stream, t);
-    if (k.gd1) return launch_gd1(o, &k, s, stream, t, ctr, gx);
+    if (k.gd1) return launch_gd1(o, &k, s, stream, t);
 
     if (op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN) {
         Exl3c4Launch a;
         base_args(o, &k, s, &a);
-        for (int c = 0; c < o->n_class; ++c) a.cls[c] = o->cls[c];
         a.row_info = (int32_t*)(s + k.row_info);
         a.a_rot = op == EXL3C4_GATE_UP ? o->a_rot : 0;
         a.h_rot = o->h_rot;
@@ -479,7 +532,7 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
             Exl3c4Launch e = a;
             e.h_rot = 1;
             e.y = s + k.h;
-            e.y_pitch = k.h_pitch;
+            e.y_pitch = (int32_t)k.h_pitch;
             e.nblk = (int32_t)(max_rows(o) / 256);
             if ((rc = exl3c4_dev_gepi(&e, stream, EV(EXL3C4_K_EPI_GU))) != 0) return rc;
         }
@@ -489,11 +542,11 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
      * (include/exl3_abi.h:751-800; h crosses rotated) */
     Exl3c4Launch d;
     base_args(o, &k, s, &d);
-    down_classes(o, &d);
+    d.dn_gd = op == EXL3C4_GU_DN;
     if (op == EXL3C4_GU_DN && k.h_gepi) {
         d.row_info = (int32_t*)(s + k.row_info);     /* written by gate_up's GEMM */
         d.x = s + k.h;                               /* h, rotated: staged as given */
-        d.x_pitch = k.h_pitch;
+        d.x_pitch = (int32_t)k.h_pitch;
         d.x_rows = (int32_t)o->T;
         d.h_rot = 1;
     } else if (op == EXL3C4_GU_DN) {
@@ -506,18 +559,18 @@ static int launch_impl(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, 
     d.nblk = (int32_t)(o->y_cols / 128);
     d.lds_pitch = k.dn_lds_pitch;
     d.dacc = (float*)(s + k.dacc);
-    d.dacc_pitch = k.dacc_pitch;
+    d.dacc_pitch = (int32_t)k.dacc_pitch;
     return exl3c4_dev_dn(&d, stream, EV(EXL3C4_K_DOWN));
 }
 
 int exl3c4_launch(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
-    const Timed t = { -1, NULL, NULL, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
+    const Ctx t = { -1, NULL, NULL, 0, NULL, NULL, NULL };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }
 
 int exl3c4_launch_checked(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream) {
-    const Timed t = { -1, NULL, NULL, 1 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
+    const Ctx t = { -1, NULL, NULL, 1, NULL, NULL, NULL };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }
 
 int64_t exl3c4_ctr_bytes(const Exl3c4Op* o) {
@@ -525,15 +578,15 @@ int64_t exl3c4_ctr_bytes(const Exl3c4Op* o) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     q = *o;
-    q.T = o->M * o->top_k;
+    q.T = o->M * o->top_k > o->T ? o->M * o->top_k : o->T;
+    if (q.x_rows < q.T) q.x_rows = q.T;
     if ((rc = check(&q)) != EXL3C4_OK) return rc;
-    const int64_t T = q.T > o->T ? q.T : o->T;
     /* the status word and a counter a row, then a counter line a token (exl3c4_launch_gather) */
-    return q.op == EXL3C4_GU_DN ? ALIGN_UP((T + 1 + o->M) * EXL3C4_SYNC_STRIDE * 4, 256) : 0;
+    return q.op == EXL3C4_GU_DN ? ALIGN_UP((q.T + 1 + o->M) * EXL3C4_SYNC_STRIDE * 4, 256) : 0;
 }
 
-int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
-                      int64_t ctr_bytes) {
+int exl3c4_launch_inst(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                       int64_t ctr_bytes, int32_t* fail) {
     int rc;
     if (!o) return EXL3C4_E_INVAL;
     if ((rc = check(o)) != EXL3C4_OK) return rc;
@@ -541,8 +594,13 @@ int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, v
     carve(o, o->T, &k);
     if (k.gd1 && ctr && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
         return EXL3C4_E_SCRATCH;
-    const Timed t = { -1, NULL, NULL, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL, NULL);
+    const Ctx t = { -1, NULL, NULL, 0, k.gd1 ? (int32_t*)ctr : NULL, NULL, fail };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
+}
+
+int exl3c4_launch_ctr(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
+                      int64_t ctr_bytes) {
+    return exl3c4_launch_inst(o, scratch, scratch_bytes, stream, ctr, ctr_bytes, NULL);
 }
 
 int exl3c4_launch_gather(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes, void* stream, void* ctr,
@@ -552,7 +610,7 @@ int exl3c4_launch_gather(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes
     if ((rc = check(o)) != EXL3C4_OK) return rc;
     if (o->op != EXL3C4_GU_DN && o->op != EXL3C4_DOWN) return EXL3C4_E_INVAL;   /* y must be down's bf16 output */
     if (!expert_w || !row_of || !out) return EXL3C4_E_INVAL;
-    if (out_pitch < o->y_cols) return EXL3C4_E_STRIDE;                         /* exl3c4_moe_gather's refusals */
+    if (out_pitch < o->y_cols || out_pitch > INT32_MAX) return EXL3C4_E_STRIDE;  /* exl3c4_moe_gather's refusals */
     if ((uintptr_t)o->y % 16 || (o->y_pitch * 2) % 16 || (uintptr_t)out % 16 || (out_pitch * 2) % 16 ||
         (uintptr_t)expert_w % 4 || (uintptr_t)row_of % 4)
         return EXL3C4_E_ALIGN;
@@ -563,11 +621,11 @@ int exl3c4_launch_gather(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes
         return EXL3C4_E_SCRATCH;
     if (k.gd1 && ctr && !fuse && (ctr_bytes < (o->T + 1) * EXL3C4_SYNC_STRIDE * 4 || (uintptr_t)ctr % 256))
         return EXL3C4_E_SCRATCH;
-    const Timed t = { -1, NULL, NULL, 0 };
     const Gather gx = { expert_w, row_of, out, out_pitch };
-    if (fuse) return launch_impl(o, scratch, scratch_bytes, stream, &t, (int32_t*)ctr, &gx);
-    if ((rc = launch_impl(o, scratch, scratch_bytes, stream, &t, k.gd1 ? (int32_t*)ctr : NULL, NULL)) != EXL3C4_OK)
-        return rc;
+    const Ctx tf = { -1, NULL, NULL, 0, (int32_t*)ctr, &gx, NULL };
+    if (fuse) return launch_impl(o, scratch, scratch_bytes, stream, &tf);
+    const Ctx t = { -1, NULL, NULL, 0, k.gd1 ? (int32_t*)ctr : NULL, NULL, NULL };
+    if ((rc = launch_impl(o, scratch, scratch_bytes, stream, &t)) != EXL3C4_OK) return rc;
     return exl3c4_moe_gather(o->y, EXL3C4_BF16, o->y_pitch, expert_w, row_of, o->M, o->top_k, o->y_cols, out,
                              out_pitch, stream);
 }
@@ -580,8 +638,8 @@ int exl3c4_launch_timed(const Exl3c4Op* o, void* scratch, int64_t scratch_bytes,
     Carve k;
     carve(o, o->T, &k);
     if (!runs_kernel(o, &k, kernel)) return EXL3C4_E_INVAL;
-    const Timed t = { kernel, ev_start, ev_stop, 0 };
-    return launch_impl(o, scratch, scratch_bytes, stream, &t, NULL, NULL);
+    const Ctx t = { kernel, ev_start, ev_stop, 0, NULL, NULL, NULL };
+    return launch_impl(o, scratch, scratch_bytes, stream, &t);
 }
 
 int exl3c4_scratch_partials(const Exl3c4Op* o, int32_t gemm, int64_t* offset, int64_t* pitch, int64_t* split_stride,

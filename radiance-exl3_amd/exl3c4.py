@@ -53,6 +53,10 @@ def lib():
         L = C.CDLL(LIB_PATH)
         L.exl3c4_scratch_bytes.restype = _i64
         L.exl3c4_scratch_bytes.argtypes = [C.POINTER(Op)]
+        L.exl3c4_launch_scratch_bytes.restype = _i64
+        L.exl3c4_launch_scratch_bytes.argtypes = [C.POINTER(Op)]
+        L.exl3c4_scratch_bytes_geom.restype = _i64
+        L.exl3c4_scratch_bytes_geom.argtypes = [_i32, _i32, C.POINTER(_i32), C.POINTER(_i32), _i64, _i64, _i64]
         L.exl3c4_launch.restype = C.c_int
         L.exl3c4_launch.argtypes = [C.POINTER(Op), _p, _i64, _p]
         L.exl3c4_launch_checked.restype = C.c_int
@@ -225,6 +229,11 @@ def make_op(op, bits, cb, classes, x, sorted_tok, expert_offset, y, M, top_k, h_
 
 def scratch_bytes(o: Op) -> int:
     return int(lib().exl3c4_scratch_bytes(C.byref(o)))
+
+
+def launch_scratch_bytes(o: Op) -> int:
+    """The scratch this launch (its T rows) needs; exl3c4_launch refuses below it."""
+    return int(lib().exl3c4_launch_scratch_bytes(C.byref(o)))
 
 
 def launch(o: Op, scratch=None, stream=None) -> int:

@@ -74,44 +74,7 @@ def test_the_library_exports_every_declared_entry_point():
 
 
 # ------------------------------------------------------------------------------------------ refusals (host only)
-class _T:
-    """A stand-in for a device tensor: a fake address and a shape; the refusals are decided before any device call."""
-
-    def __init__(self, shape, addr=0x10000, elem=2):
-        self.shape, self._addr, self._elem = shape, addr, elem
-
-    def data_ptr(self):
-        return self._addr
-
-    def stride(self, d):
-        s = 1
-        for x in self.shape[d + 1:]:
-            s *= x
-        return s
-
-    def element_size(self):
-        return self._elem
-
-    def numel(self):
-        n = 1
-        for x in self.shape:
-            n *= x
-        return n
-
-
-def _op(op=exl3c4.GATE_UP, bits=4, cb="mul1", H=256, W=128, E=4, M=2, top_k=2, h_rot=0, a_rot=0, ycols=None,
-        xcols=None):
-    rows, cols = (2 * W, H) if op in (exl3c4.GATE_UP, exl3c4.PREP_GU, exl3c4.GU_DN) else (H, W)
-    rec = _T((E, rows * cols * bits // 8), elem=1)
-    c = exl3c4.make_class(rows, cols, codes=rec, suh=_T((E, cols)), suh1=_T((E, cols)), svh=_T((E, rows)),
-                          dn_suh=_T((E, W)))
-    T = M * top_k
-    x = _T((M if op != exl3c4.DOWN and not a_rot else T, xcols or (2 * cols if a_rot else cols)))
-    yc = ycols or {exl3c4.GATE_UP: W, exl3c4.DOWN: H, exl3c4.PREP_GU: 2 * H, exl3c4.GU_DN: H}[op]
-    y = _T((T, yc))
-    dn = [exl3c4.make_class(H, W, codes=rec, svh=_T((E, H)))] if op == exl3c4.GU_DN else None
-    return exl3c4.make_op(op, bits, cb, [c], x, _T((T,), elem=4), _T((E + 1,), elem=4), y, M, top_k, h_rot=h_rot,
-                          a_rot=a_rot, dn=dn)
+from hostops import Fake as _T, op as _op  # noqa: E402
 
 
 def _launch_rc(o, scratch=None, nbytes=0):
