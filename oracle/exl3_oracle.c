@@ -444,7 +444,14 @@ static int64_t y_cols_of(const OrOp* o) {
     return o->op == 2 ? 2 * x : o->op == 1 ? r / 2 : r;
 }
 
-/* kernels/exl3ref/ref.c:307-331: zero every output row (not prep_gu's), then each live expert's rows once. */
+/* Threads or_launch spreads the experts over (OpenMP): 1 unless a caller asks for more. Each expert's rows are one
+ * thread's, computed exactly as on one thread, so the bits do not depend on the count. */
+static int g_threads = 1;
+void or_set_threads(int n) { g_threads = n > 0 ? n : 1; }
+int  or_get_threads(void) { return g_threads; }
+
+/* kernels/exl3ref/ref.c:307-331: zero every output row (not prep_gu's), then each live expert's rows once -- the
+ * experts independent of each other, so a thread each (one decode of W_hat a live expert, as the reference does). */
 int or_launch(const OrOp* o) {
     const int64_t y_cols = y_cols_of(o);
     int64_t most = 0, widest = 0, xc = 0;
@@ -457,20 +464,27 @@ int or_launch(const OrOp* o) {
         if (o->cls[c].cols > xc) xc = o->cls[c].cols;
     }
     const int64_t row = xc > widest ? xc : widest;
-    Work w = { malloc((size_t)(most + 1) * sizeof(float)), malloc((size_t)(row + 1) * sizeof(float)),
-               malloc((size_t)(row + 1) * sizeof(float)), malloc((size_t)(widest + 1) * sizeof(float)) };
-    if (!w.what || !w.x || !w.xr || !w.acc) rc = OR_E_NOMEM;
-    for (int64_t e = 0; e < o->n_expert && rc == OR_OK; ++e) {
-        const int64_t lo = o->expert_offset[e], hi = o->expert_offset[e + 1];
-        int live = 0;
-        for (int64_t i = lo; i < hi && !live; ++i) live = o->sorted_tok[i] >= 0;
-        if (o->op == 2) {
-            if (hi > lo) prep_rows(o, e, &w);
-        } else if (live) {
-            rc = expert_rows(o, e, &w);
+#pragma omp parallel num_threads(g_threads)
+    {
+        Work w = { malloc((size_t)(most + 1) * sizeof(float)), malloc((size_t)(row + 1) * sizeof(float)),
+                   malloc((size_t)(row + 1) * sizeof(float)), malloc((size_t)(widest + 1) * sizeof(float)) };
+        int mine = (!w.what || !w.x || !w.xr || !w.acc) ? OR_E_NOMEM : OR_OK;
+#pragma omp for schedule(dynamic, 1)
+        for (int64_t e = 0; e < o->n_expert; ++e) {
+            if (mine != OR_OK) continue;
+            const int64_t lo = o->expert_offset[e], hi = o->expert_offset[e + 1];
+            int live = 0;
+            for (int64_t i = lo; i < hi && !live; ++i) live = o->sorted_tok[i] >= 0;
+            if (o->op == 2) {
+                if (hi > lo) prep_rows(o, e, &w);
+            } else if (live) {
+                mine = expert_rows(o, e, &w);
+            }
         }
+#pragma omp critical
+        if (mine != OR_OK && rc == OR_OK) rc = mine;
+        free(w.what); free(w.x); free(w.xr); free(w.acc);
     }
-    free(w.what); free(w.x); free(w.xr); free(w.acc);
     return rc;
 }
 

@@ -101,6 +101,11 @@ typedef struct OrOp {
     int64_t        T, y_pitch;
 } OrOp;
 
+/* Threads or_launch / or_gate_up_down spread the live experts over (OpenMP; default 1, the reference's serial loop).
+ * The outputs do not depend on it: each expert's rows are computed by one thread in the serial order. */
+void or_set_threads(int n);
+int  or_get_threads(void);
+
 /* Runs one op as kernels/exl3ref/ref.c:278-331 does (after its refusals: this entry assumes operands already
  * checked). Returns OR_OK, or OR_E_SHAPE / OR_E_NOMEM. */
 int or_launch(const OrOp* o);

@@ -42,6 +42,8 @@ _i64 = C.c_int64
 
 
 def _declare(L):
+    L.or_set_threads.argtypes = [C.c_int]
+    L.or_get_threads.restype = C.c_int
     L.or_half_to_float.restype = C.c_float
     L.or_half_to_float.argtypes = [C.c_uint16]
     L.or_half_from_double.restype = C.c_uint16
@@ -96,6 +98,24 @@ def _ptr(a: np.ndarray):
 
 
 # ------------------------------------------------------------------------------------------ scalar helpers
+def set_threads(n: int) -> None:
+    """Threads the op-level oracle spreads live experts over (the outputs do not depend on it)."""
+    lib().or_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().or_get_threads())
+
+
+def default_threads() -> int:
+    """The host's cores, at most 16 (the GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
 def half_from_double(x: float) -> int:
     return int(lib().or_half_from_double(float(x)))
 

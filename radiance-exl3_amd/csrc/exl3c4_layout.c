@@ -17,65 +17,81 @@
 
 #include "exl3c4.h"
 
-static void tile_map(int tr[256], int tc[256]) {
-    for (int p = 0; p < 256; ++p) {
-        const int L = p >> 3, j = p & 7;
-        tr[p] = 2 * (L & 3) + ((j & 1) | ((j & 2) << 2));
-        tc[p] = (L >> 2) + 8 * (j >> 2);
-    }
-}
+/* Trellis position p = 8 L + j sits at tile row 2 (L % 4) + {0, 1, 8, 9}[j % 4], column L / 4 + 8 (j / 4)
+ * (common/exl3_decode.c:71-76). */
+#define TILE_R(p) (2 * (((p) >> 3) & 3) + (((p) & 1) | (((p) & 2) << 2)))
+#define TILE_C(p) (((p) >> 5) + 8 * (((p) >> 2) & 1))
 
-/* Tile (tk, tn)'s 8 K stream words from the plane: its 16 rows' 2 K bytes each, symbols LSB first, then the stream. */
-static void tile_words(const uint8_t* codes, int64_t rb, int64_t tk, int64_t tn, int bits, const int* tr,
-                       const int* tc, uint32_t* w) {
+/* The two directions are written once for a constant K (always inlined into one copy a K, so the tile map, the masks
+ * and the shifts fold to constants and the symbol loops unroll): at K = 4 a tile converts in about a tenth of the
+ * time of the same loops with K and the map read at run time. */
+#define INLINE static inline __attribute__((always_inline))
+
+/* Tile (tk, tn)'s 8 K stream words from the plane: its 16 rows' 2 K bytes each, symbols LSB first, then the stream
+ * (MSB first: position 0 in the top bits of word 0). */
+INLINE void tile_words(const uint8_t* codes, int64_t rb, int64_t tk, int64_t tn, const int bits, uint32_t* w) {
     uint8_t sym[16][16];   /* [c][r]: row n = 16 tn + c, column k = 16 tk + r */
     const uint32_t mask = (1u << bits) - 1u;
     const int seg = 2 * bits;
     for (int c = 0; c < 16; ++c) {
         uint8_t b[18] = { 0 };
         memcpy(b, codes + (tn * 16 + c) * rb + tk * seg, (size_t)seg);
+        uint64_t lo = 0, hi = 0;                          /* the row's 16 K bits, little-endian */
+        memcpy(&lo, b, 8);
+        memcpy(&hi, b + 8, 8);
         for (int r = 0; r < 16; ++r) {
             const int o = r * bits;
-            sym[c][r] = (uint8_t)((((uint32_t)b[o >> 3] | ((uint32_t)b[(o >> 3) + 1] << 8)) >> (o & 7)) & mask);
+            const uint64_t v = o < 64 ? (lo >> o) | (o > 0 && o + bits > 64 ? hi << (64 - o) : 0) : hi >> (o - 64);
+            sym[c][r] = (uint8_t)(v & mask);
         }
     }
-    uint64_t acc = 0;
-    int nb = 0;
-    for (int p = 0; p < 256; ++p) {
-        acc = (acc << bits) | sym[tc[p]][tr[p]];
-        nb += bits;
-        if (nb >= 32) {
-            nb -= 32;
-            *w++ = (uint32_t)(acc >> nb);
-            acc &= (nb ? ((1ull << nb) - 1ull) : 0ull);
+    for (int s = 0; s < 8; ++s) {                         /* segment s: positions 32 s .. 32 s + 31, K words */
+        uint64_t acc = 0;
+        int nb = 0;
+        for (int p = 32 * s; p < 32 * s + 32; ++p) {
+            acc = (acc << bits) | sym[TILE_C(p)][TILE_R(p)];
+            nb += bits;
+            if (nb >= 32) {
+                nb -= 32;
+                *w++ = (uint32_t)(acc >> nb);
+                acc &= (1ull << nb) - 1ull;
+            }
         }
     }
 }
 
-static void words_tile(const uint32_t* w, int64_t tk, int64_t tn, int bits, const int* tr, const int* tc,
-                       uint8_t* codes, int64_t rb) {
+INLINE void words_tile(const uint32_t* w, int64_t tk, int64_t tn, const int bits, uint8_t* codes, int64_t rb) {
     uint8_t sym[16][16];
     const uint32_t mask = (1u << bits) - 1u;
-    uint64_t acc = 0;
-    int nb = 0;
-    for (int p = 0; p < 256; ++p) {
-        if (nb < bits) {
-            acc = (acc << 32) | *w++;
-            nb += 32;
+    for (int s = 0; s < 8; ++s) {
+        uint64_t acc = 0;
+        int nb = 0;
+        for (int p = 32 * s; p < 32 * s + 32; ++p) {
+            if (nb < bits) {
+                acc = (acc << 32) | *w++;
+                nb += 32;
+            }
+            nb -= bits;
+            sym[TILE_C(p)][TILE_R(p)] = (uint8_t)((acc >> nb) & mask);
+            acc &= (1ull << nb) - 1ull;
         }
-        nb -= bits;
-        sym[tc[p]][tr[p]] = (uint8_t)((acc >> nb) & mask);
-        acc &= (nb ? ((1ull << nb) - 1ull) : 0ull);
     }
     const int seg = 2 * bits;
     for (int c = 0; c < 16; ++c) {
-        uint8_t b[18] = { 0 };
+        uint64_t lo = 0, hi = 0;
         for (int r = 0; r < 16; ++r) {
             const int o = r * bits;
-            const uint32_t v = (uint32_t)sym[c][r] << (o & 7);
-            b[o >> 3] |= (uint8_t)v;
-            b[(o >> 3) + 1] |= (uint8_t)(v >> 8);
+            const uint64_t v = sym[c][r];
+            if (o < 64) {
+                lo |= v << o;
+                if (o + bits > 64) hi |= v >> (64 - o);
+            } else {
+                hi |= v << (o - 64);
+            }
         }
+        uint8_t b[16];
+        memcpy(b, &lo, 8);
+        memcpy(b + 8, &hi, 8);
         memcpy(codes + (tn * 16 + c) * rb + tk * seg, b, (size_t)seg);
     }
 }
@@ -94,38 +110,58 @@ static int64_t seg_at(int64_t tk, int64_t tn, int s, int64_t ksteps, int bits) {
     return ((nb * ksteps + ks) * 64 + X) * bits;
 }
 
-int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64_t cols, int32_t bits, void* record) {
-    int tr[256], tc[256];
+INLINE void relayout_k(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64_t cols, const int bits,
+                       uint32_t* out) {
     uint32_t w[64];
-    if (!codes || !record) return EXL3C4_E_INVAL;
-    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
-    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
-    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
-    tile_map(tr, tc);
-    uint32_t* out = (uint32_t*)record;
     const int64_t ksteps = cols / 64;
     for (int64_t tn = 0; tn < rows / 16; ++tn)
         for (int64_t tk = 0; tk < cols / 16; ++tk) {
-            tile_words(codes, row_bytes, tk, tn, bits, tr, tc, w);
+            tile_words(codes, row_bytes, tk, tn, bits, w);
             for (int s = 0; s < 8; ++s) memcpy(out + seg_at(tk, tn, s, ksteps, bits), w + s * bits, (size_t)bits * 4);
         }
-    return EXL3C4_OK;
 }
 
-int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes) {
-    int tr[256], tc[256];
+INLINE void unrelayout_k(const uint32_t* in, int64_t rows, int64_t cols, const int bits, uint8_t* codes,
+                         int64_t row_bytes) {
     uint32_t w[64];
-    if (!codes || !record) return EXL3C4_E_INVAL;
-    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
-    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
-    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
-    tile_map(tr, tc);
-    const uint32_t* in = (const uint32_t*)record;
     const int64_t ksteps = cols / 64;
     for (int64_t tn = 0; tn < rows / 16; ++tn)
         for (int64_t tk = 0; tk < cols / 16; ++tk) {
             for (int s = 0; s < 8; ++s) memcpy(w + s * bits, in + seg_at(tk, tn, s, ksteps, bits), (size_t)bits * 4);
-            words_tile(w, tk, tn, bits, tr, tc, codes, row_bytes);
+            words_tile(w, tk, tn, bits, codes, row_bytes);
         }
+}
+
+#define BY_K(CALL)                                                                                                   \
+    switch (bits) {                                                                                                  \
+    case 1: CALL(1); break;                                                                                          \
+    case 2: CALL(2); break;                                                                                          \
+    case 3: CALL(3); break;                                                                                          \
+    case 4: CALL(4); break;                                                                                          \
+    case 5: CALL(5); break;                                                                                          \
+    case 6: CALL(6); break;                                                                                          \
+    case 7: CALL(7); break;                                                                                          \
+    default: CALL(8); break;                                                                                         \
+    }
+
+int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64_t cols, int32_t bits, void* record) {
+    if (!codes || !record) return EXL3C4_E_INVAL;
+    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
+    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
+    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
+#define RL(K) relayout_k(codes, row_bytes, rows, cols, K, (uint32_t*)record)
+    BY_K(RL)
+#undef RL
+    return EXL3C4_OK;
+}
+
+int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes) {
+    if (!codes || !record) return EXL3C4_E_INVAL;
+    if (!shape_ok(rows, cols, bits)) return bits < 1 || bits > 8 ? EXL3C4_E_DTYPE : EXL3C4_E_SHAPE;
+    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
+    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
+#define URL(K) unrelayout_k((const uint32_t*)record, rows, cols, K, codes, row_bytes)
+    BY_K(URL)
+#undef URL
     return EXL3C4_OK;
 }

@@ -2,7 +2,9 @@
 
 A case is numpy data only (canonical planes, scales, routing, activations). `oracle_*` run the CPU restatement;
 `Dev` uploads the case (codes through the library's own relayout, as a loader would) and runs the device ops through
-the C-ABI (radiance-exl3_amd/exl3c4.py).
+the C-ABI (radiance-exl3_amd/exl3c4.py). Every device output, scratch and counter block sits between two poisoned
+256-byte margins, and every launch is followed by a check that the margins and the op's inputs are unchanged (the
+reference harness's redzones, tests/ref/exl3ref_run.cpp:30-33, 56-57).
 """
 from __future__ import annotations
 
@@ -10,6 +12,10 @@ import numpy as np
 
 import exl3c4_synth as syn
 import oracle
+
+oracle.set_threads(oracle.default_threads())      # the checker's experts over the host's cores (same bits)
+MARGIN = 256
+POISON = 0xA5
 
 
 class Expert:
@@ -26,20 +32,35 @@ class Case:
     """n_expert experts of n_class classes: gate_up [2W_c, H_c] and down [H_c, W_c] per expert, class c = e % n_class."""
 
     def __init__(self, seed, n_tok, top_k, n_expert, geoms, bits, cb, drop=0.0, protect_tail=0, x_bf16=False,
-                 routing="uniform", expert_ids=None):
+                 routing="uniform", expert_ids=None, dn_bits=None):
         rng = np.random.default_rng(seed)
         self.rng = rng
-        self.n_tok, self.top_k, self.n_expert, self.bits, self.cb = n_tok, top_k, n_expert, bits, cb
+        self.n_expert, self.bits, self.cb = n_expert, bits, cb
+        self.dn_bits = bits if dn_bits is None else dn_bits    # down's K (a layer of mixed K: gate_up then down)
         self.n_class = len(geoms)
         self.geoms = geoms                                  # per class (H, W): hidden, width
         self.gu, self.dn = [], []
         for e in range(n_expert):
             H, W = geoms[e % self.n_class]
             g = Expert(rng, 2 * W, H, bits, True)
-            d = Expert(rng, H, W, bits, False)
+            d = Expert(rng, H, W, self.dn_bits, False)
             g.dn_suh = d.suh                                # down's suh of the same expert
             self.gu.append(g)
             self.dn.append(d)
+        self.route(rng, n_tok, top_k, drop, protect_tail, x_bf16, routing, expert_ids)
+
+    def rerouted(self, seed, n_tok, top_k, drop=0.0, protect_tail=0, x_bf16=False, routing="uniform",
+                 expert_ids=None):
+        """The same experts under another routing draw and batch (a shallow copy: the experts are shared)."""
+        c = object.__new__(Case)
+        c.__dict__.update(self.__dict__)
+        c.rng = np.random.default_rng(seed)
+        c.route(c.rng, n_tok, top_k, drop, protect_tail, x_bf16, routing, expert_ids)
+        return c
+
+    def route(self, rng, n_tok, top_k, drop, protect_tail, x_bf16, routing, expert_ids):
+        n_expert, geoms = self.n_expert, self.geoms
+        self.n_tok, self.top_k = n_tok, top_k
         Hmax = max(h for h, _ in geoms)
         self.x_bf16 = x_bf16
         x = rng.standard_normal((n_tok, Hmax)).astype(np.float32)
@@ -68,9 +89,18 @@ class Case:
 
     # ------------------------------------------------------------------ class tables (numpy, stacked)
     def classes(self, which):
+        """Class c's stacked tables (experts e % n_class == c at entry e / n_class), cached by the identity of the
+        experts' arrays (a test that replaces one gets fresh tables)."""
+        experts = self.gu if which == "gu" else self.dn
+        key = (which, tuple((id(x.codes), id(x.suh), id(x.svh), id(getattr(x, "suh1", None)),
+                             id(getattr(x, "dn_suh", None))) for x in experts))
+        cache = self.__dict__.setdefault("_cls_cache", {})
+        hit = cache.get(which)
+        if hit is not None and hit[0] == key:
+            return hit[1]
         out = []
         for c in range(self.n_class):
-            ex = [(self.gu if which == "gu" else self.dn)[e] for e in range(c, self.n_expert, self.n_class)]
+            ex = [experts[e] for e in range(c, self.n_expert, self.n_class)]
             d = {"rows": ex[0].rows, "cols": ex[0].cols,
                  "codes": np.stack([x.codes for x in ex]), "suh": np.stack([x.suh for x in ex]),
                  "svh": np.stack([x.svh for x in ex])}
@@ -78,6 +108,7 @@ class Case:
                 d["suh1"] = np.stack([x.suh1 for x in ex])
                 d["dn_suh"] = np.stack([x.dn_suh for x in ex])
             out.append(d)
+        cache[which] = (key, out)                       # one set of tables a side at a time (large cases)
         return out
 
     # ------------------------------------------------------------------ the oracle
@@ -93,7 +124,7 @@ class Case:
                              self.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=self.x_bf16 and not a_rot)
 
     def oracle_down(self, h, h_rot=0):
-        return oracle.run_op(oracle.OP_DOWN, self.classes("dn"), self.bits, self.cb, h, self.sorted_tok, self.off,
+        return oracle.run_op(oracle.OP_DOWN, self.classes("dn"), self.dn_bits, self.cb, h, self.sorted_tok, self.off,
                              self.top_k, h_rot=h_rot)
 
     def h_rot_of(self, h0):
@@ -138,7 +169,7 @@ class Case:
         out = np.zeros((self.T, N), np.float32)
         for e, rows in self.live_rows().items():
             d = self.dn[e]
-            what = oracle.what_rows(d.codes, d.rows, d.cols, self.bits, self.cb)
+            what = oracle.what_rows(d.codes, d.rows, d.cols, self.dn_bits, self.cb)
             x = f16(h[rows, :d.cols])
             if not h_rot:
                 x = np.stack([oracle.prologue(r, d.suh) for r in x])
@@ -146,6 +177,7 @@ class Case:
         return out
 
     def oracle_gate_up_down(self):
+        assert self.dn_bits == self.bits, "gate_up_down runs one K; a mixed-K layer is gate_up then down"
         return oracle.run_gate_up_down(self.classes("gu"), self.classes("dn"), self.bits, self.cb, self.x,
                                        self.sorted_tok, self.off, self.top_k, x_bf16=self.x_bf16)
 
@@ -198,31 +230,80 @@ def rel_err(got, want):
     return float(np.max(np.abs(got.astype(np.float64) - want.astype(np.float64)))) / max(rms, 1e-30)
 
 
-class Dev:
-    """A case uploaded to the device: stacked stored records and scales, routing, activations."""
+class Guard:
+    """A device buffer between two poisoned MARGIN-byte margins: `view` is the interior (256-byte aligned, as the
+    allocator aligns the whole); ok() checks that nothing wrote into the margins."""
 
-    def __init__(self, case: Case):
+    def __init__(self, torch, nbytes, fill=None):
+        self.torch = torch
+        self.n = int(nbytes)
+        self.base = torch.full((self.n + 2 * MARGIN,), POISON, dtype=torch.uint8, device="cuda")
+        assert self.base.data_ptr() % 256 == 0
+        self.view = self.base[MARGIN:MARGIN + self.n]
+        if fill is not None:
+            self.view.fill_(fill)
+
+    def ok(self):
+        t = self.torch
+        return bool(t.all(self.base[:MARGIN] == POISON)) and bool(t.all(self.base[MARGIN + self.n:] == POISON))
+
+
+class Dev:
+    """A case uploaded to the device: stacked stored records and scales, routing, activations. Outputs, scratch and
+    counter blocks are guarded (Guard); after every launch the margins and the inputs are checked unchanged."""
+
+    def __init__(self, case: Case, share: "Dev | None" = None):
         import torch
         import exl3c4
         self.case = case
         self.torch, self.ex = torch, exl3c4
         dev = "cuda"
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
-        self.tabs = {}
-        for which in ("gu", "dn"):
-            cls = []
-            for c in case.classes(which):
-                recs = np.stack([exl3c4.relayout(codes, c["rows"], c["cols"], case.bits) for codes in c["codes"]])
-                d = {"rows": c["rows"], "cols": c["cols"], "codes": t(recs),
-                     "suh": t(c["suh"].view(np.uint16)), "svh": t(c["svh"].view(np.uint16))}
-                if which == "gu":
-                    d["suh1"] = t(c["suh1"].view(np.uint16))
-                    d["dn_suh"] = t(c["dn_suh"].view(np.uint16))
-                cls.append(d)
-            self.tabs[which] = cls
+        self._guards = []
+        if share is not None:                           # the same experts (Case.rerouted): share their tables
+            self.tabs, self._sums = share.tabs, share._sums
+        else:
+            self.tabs = {}
+            for which in ("gu", "dn"):
+                bits = case.bits if which == "gu" else case.dn_bits
+                cls = []
+                for c in case.classes(which):
+                    recs = np.stack([exl3c4.relayout(codes, c["rows"], c["cols"], bits) for codes in c["codes"]])
+                    d = {"rows": c["rows"], "cols": c["cols"], "codes": t(recs),
+                         "suh": t(c["suh"].view(np.uint16)), "svh": t(c["svh"].view(np.uint16))}
+                    if which == "gu":
+                        d["suh1"] = t(c["suh1"].view(np.uint16))
+                        d["dn_suh"] = t(c["dn_suh"].view(np.uint16))
+                    cls.append(d)
+                self.tabs[which] = cls
+            self._sums = self._table_sums()
         self.x = t(case.x.astype(np.uint16).view(np.int16))
         self.sorted_tok = t(case.sorted_tok)
         self.off = t(case.off)
+        self._inputs = (self.x.clone(), self.sorted_tok.clone(), self.off.clone())
+
+    def _table_sums(self):
+        torch = self.torch
+        return [int(torch.sum(v.view(torch.uint8).to(torch.int64))) for w in ("gu", "dn") for d in self.tabs[w]
+                for k, v in sorted(d.items()) if k not in ("rows", "cols")]
+
+    def guard(self, nbytes, fill=None):
+        g = Guard(self.torch, nbytes, fill)
+        self._guards.append(g)
+        return g
+
+    def check_guards(self, what=""):
+        """Every guarded buffer's margins intact, and the op's inputs (activations, routing, tables) unchanged."""
+        torch = self.torch
+        torch.cuda.synchronize()
+        bad = [i for i, g in enumerate(self._guards) if not g.ok()]
+        assert not bad, f"{what}: a launch wrote into the margins of guarded buffer(s) {bad}"
+        x, st, off = self._inputs
+        assert torch.equal(self.x, x) and torch.equal(self.sorted_tok, st) and torch.equal(self.off, off), \
+            f"{what}: a launch changed its input rows or routing"
+
+    def check_tables(self):
+        assert self._table_sums() == self._sums, "a launch changed a weight table"
 
     def cls(self, which, dn_suh=True):
         out = []
@@ -231,38 +312,53 @@ class Dev:
                                           svh=d["svh"], dn_suh=d.get("dn_suh") if dn_suh else None))
         return out
 
+    def scratch(self, o, exact=False):
+        """Guarded scratch of the band's size (or exactly this launch's, `exact`), its interior poisoned with 0xFF
+        (NaN as f32 and f16): a kernel that read scratch it had not written would show."""
+        n = self.ex.launch_scratch_bytes(o) if exact else self.ex.scratch_bytes(o)
+        assert n >= 0, f"scratch_bytes {self.ex.STATUS.get(n, n)}"
+        return self.guard(max(n, 256), fill=0xFF).view
+
     def _run(self, o, y, *inputs, expect=0):
         """Launches `o` (whose output is `y`); `inputs`: device tensors the op points to that the caller made for it,
         kept alive with it so that last_acc can launch it again."""
-        s = self.ex.alloc_scratch(o)
+        s = self.scratch(o)
         rc = self.ex.launch(o, s)
         assert rc == expect, f"launch status {self.ex.STATUS.get(rc, rc)}"
         self.torch.cuda.synchronize()
         self.last = (o, y, inputs)
         self.status = self.ex.launch_status(o, s) if rc == 0 else None
         assert self.status in (None, 0), f"gate_up_down's single kernel left status {self.status}"
+        self.check_guards("launch")
 
     def last_acc(self, gemm=0):
         """The f32 accumulations of the last launch: the same op again through exl3c4_launch_checked (which also
         leaves the prefill GEMMs' sums in scratch), whose output must be the production launch's, bit for bit."""
         o, y, _ = self.last
         before = y.clone()
-        s = self.ex.alloc_scratch(o)
+        s = self.scratch(o)
         rc = self.ex.launch_checked(o, s)
         assert rc == 0, f"launch_checked status {self.ex.STATUS.get(rc, rc)}"
         self.torch.cuda.synchronize()
         assert self.torch.equal(y, before), "exl3c4_launch_checked wrote another output than exl3c4_launch"
+        self.check_guards("launch_checked")
         return self.ex.partial_sums(o, s, gemm)
 
-    def out(self, cols, fill=0x7E7E):
-        return self.torch.full((self.case.T, cols), fill, dtype=self.torch.int16, device="cuda")
+    def out(self, cols, fill=0x7E7E, rows=None):
+        """A guarded int16 output [rows (default T), cols], prefilled with `fill` (a sentinel the op must overwrite
+        where it writes)."""
+        rows = self.case.T if rows is None else rows
+        g = self.guard(rows * cols * 2)
+        v = g.view.view(self.torch.int16).view(rows, cols)
+        v.fill_(int(np.int16(np.uint16(fill).view(np.int16))))
+        return v
 
     def prep(self, prefill=0xFFFF):
         c = self.case
         C = max(d["cols"] for d in self.tabs["gu"])
-        y = self.out(2 * C, fill=np.int16(np.uint16(prefill).view(np.int16)))
+        y = self.out(2 * C, fill=prefill)
         o = self.ex.make_op(self.ex.PREP_GU, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
-                            c.n_tok, c.top_k, x_bf16=c.x_bf16)
+                            c.n_tok, c.top_k, x_bf16=c.x_bf16, n_expert=c.n_expert)
         self._run(o, y)
         return y.cpu().numpy().view(np.uint16)
 
@@ -272,7 +368,8 @@ class Dev:
         y = self.out(W)
         x = xr if a_rot else self.x
         o = self.ex.make_op(self.ex.GATE_UP, c.bits, c.cb, self.cls("gu"), x, self.sorted_tok, self.off, y,
-                            c.n_tok, c.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=c.x_bf16 and not a_rot)
+                            c.n_tok, c.top_k, h_rot=h_rot, a_rot=a_rot, x_bf16=c.x_bf16 and not a_rot,
+                            n_expert=c.n_expert)
         self._run(o, y, x)
         return y.cpu().numpy().view(np.uint16)
 
@@ -281,18 +378,22 @@ class Dev:
         N = max(d["rows"] for d in self.tabs["dn"])
         y = self.out(N)
         hd = self.torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).to("cuda")
-        o = self.ex.make_op(self.ex.DOWN, c.bits, c.cb, self.cls("dn"), hd, self.sorted_tok, self.off, y,
-                            c.n_tok, c.top_k, h_rot=h_rot)
+        o = self.ex.make_op(self.ex.DOWN, c.dn_bits, c.cb, self.cls("dn"), hd, self.sorted_tok, self.off, y,
+                            c.n_tok, c.top_k, h_rot=h_rot, n_expert=c.n_expert)
         self._run(o, y, hd)
         return y.cpu().numpy().view(np.uint16)
 
+    def gd_op(self, y, M=None):
+        """gate_up_down's op over this case, writing y."""
+        c = self.case
+        assert c.dn_bits == c.bits
+        dn = [self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in self.tabs["dn"]]
+        return self.ex.make_op(self.ex.GU_DN, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
+                               c.n_tok if M is None else M, c.top_k, dn=dn, x_bf16=c.x_bf16, n_expert=c.n_expert)
+
     def gate_up_down(self):
         """gate_up_down's output; self.status is then None (two kernels) or 0 (one kernel, which went well)."""
-        c = self.case
         N = max(d["rows"] for d in self.tabs["dn"])
         y = self.out(N)
-        dn = [self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in self.tabs["dn"]]
-        o = self.ex.make_op(self.ex.GU_DN, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
-                            c.n_tok, c.top_k, dn=dn, x_bf16=c.x_bf16)
-        self._run(o, y)
+        self._run(self.gd_op(y), y)
         return y.cpu().numpy().view(np.uint16)

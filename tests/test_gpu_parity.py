@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 
 from cases import Case, Dev, bf16, f16, narrowed_ok, rel_err, rel_l2
+from gpuchecks import acc_ok as _acc_ok, check_all as _check_all
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-3
@@ -70,62 +71,6 @@ def test_dequant_covers_every_mul1_state_at_the_expert_geometry(torch_cuda):
 
 # ------------------------------------------------------------------------------------------ the ops
 SMALL = dict(n_tok=4, top_k=4, n_expert=8, geoms=[(256, 128)], bits=4, cb="mul1")
-
-
-def _acc_ok(got, want, case, which):
-    """The north star's bar on the f32 accumulations themselves: max-abs <= 2e-3 x RMS over each live row's own
-    columns (a narrower class's row has fewer)."""
-    g, w = [], []
-    for e, rows in case.live_rows().items():
-        n = (case.gu if which == "gu" else case.dn)[e].rows
-        g.append(got[rows, :n].ravel())
-        w.append(want[rows, :n].ravel())
-    return rel_err(np.concatenate(g), np.concatenate(w)) <= TOL
-
-
-def _check_all(case, label):
-    dev = Dev(case)
-    _say(f"{label}: prep_gu")
-    xr_d = dev.prep()
-    xr_o = case.oracle_prep()
-    assert np.array_equal(xr_d, xr_o), f"prep_gu: {np.count_nonzero(xr_d != xr_o)} elements differ"
-
-    _say(f"{label}: gate_up h_rot 0 / 1, a_rot 0 / 1")
-    h0 = dev.gate_up(h_rot=0)
-    N = max(g.rows for g in case.gu)
-    assert _acc_ok(dev.last_acc()[:, :N], case.oracle_gu_acc(xr_o), case, "gu")
-    h0_o = case.oracle_gate_up(h_rot=0)
-    assert narrowed_ok(h0, h0_o, "f16") == 0
-    assert rel_l2(f16(h0), f16(h0_o)) <= CHAIN_TOL
-    h1 = dev.gate_up(h_rot=1)
-    assert np.array_equal(h1, case.h_rot_of(h0))        # h_rot = 1 is down's first step on its own h, to the bit
-    assert rel_l2(f16(h1), f16(case.oracle_gate_up(h_rot=1))) <= CHAIN_TOL
-    xr_t = dev.torch.from_numpy(xr_d.view(np.int16)).cuda()
-    assert np.array_equal(dev.gate_up(h_rot=0, a_rot=1, xr=xr_t), h0)          # prep_gu -> gate_up(a_rot 1): same bits
-    assert np.array_equal(dev.gate_up(h_rot=1, a_rot=1, xr=xr_t), h1)
-
-    _say(f"{label}: down h_rot 0 / 1, gate_up_down")
-    y0 = dev.down(h0, h_rot=0)                         # the oracle's down on the DEVICE's h: isolates down
-    Nd = max(d.rows for d in case.dn)
-    assert _acc_ok(dev.last_acc()[:, :Nd], case.oracle_dn_acc(h0, h_rot=0), case, "dn")
-    y0_o = case.oracle_down(h0, h_rot=0)
-    assert narrowed_ok(y0, y0_o, "bf16") == 0
-    assert rel_l2(bf16(y0), bf16(y0_o)) <= CHAIN_TOL
-    y1 = dev.down(h1, h_rot=1)
-    assert np.array_equal(y1, y0)                      # the pair's bits do not depend on h_rot
-    gd = dev.gate_up_down()
-    assert np.array_equal(gd, y1)                      # gate_up_down is its pair, to the bit
-    assert rel_l2(bf16(gd), bf16(case.oracle_gate_up_down())) <= CHAIN_TOL
-    assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
-
-    # zero rows: dropped slots, rows past the live count (whatever sorted_tok holds there), outside the runs
-    T, n_live = case.T, int(case.off[-1])
-    dead = np.array([i >= n_live or i < case.off[0] or case.sorted_tok[i] < 0 for i in range(T)])
-    for out in (h0, h1, y0, gd):
-        assert np.all(out[dead] == 0)
-    # determinism: a replay writes the same bytes
-    assert np.array_equal(dev.gate_up_down(), gd)
-    return dev
 
 
 def test_ops_small_case(torch_cuda):
@@ -252,12 +197,13 @@ def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bit
                        dn=dn)
         assert case.T >= ex.GD_FUSE_MIN_T and ex.ctr_bytes(o) > 0
         if ctr is None:
-            ctr = torch.zeros(max(ex.ctr_bytes(o), 256), dtype=torch.uint8, device="cuda")
-        s = ex.alloc_scratch(o)
+            ctr = dev.guard(max(ex.ctr_bytes(o), 256), fill=0).view
+        s = dev.scratch(o)
         assert ex.launch_ctr(o, s, ctr) == 0
         torch.cuda.synchronize()
         assert int(torch.count_nonzero(ctr)) == 0, f"seed {seed}: the counter block is not zero after the launch"
         assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+        dev.check_guards(f"launch_ctr seed {seed}")
 
 
 # ------------------------------------------------------------------------------------------ the gather in the op's kernel
@@ -278,7 +224,7 @@ def test_launch_gather_gives_the_bits_of_the_launch_and_the_gather(torch_cuda, s
     import exl3c4 as ex
     import oracle
     torch = torch_cuda
-    ctr = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    ctr = None
     for rep, nt in enumerate((n_tok, max(1, n_tok - 3))):
         ids = None
         if empty:
@@ -296,23 +242,65 @@ def test_launch_gather_gives_the_bits_of_the_launch_and_the_gather(torch_cuda, s
         w = np.random.default_rng(seed + 7).random((nt, top_k)).astype(np.float32)
         wt, rt = torch.from_numpy(w).cuda(), torch.from_numpy(row_of).cuda()
         outs, ys = [], []
+        if ctr is None:                                           # one guarded counter block for both launches
+            ctr = dev.guard(1 << 16, fill=0)
         for fused in (True, False):
             y = dev.out(N, fill=0x1234)
-            out = torch.full((nt, N), 0x1234, dtype=torch.int16, device="cuda")
+            out = dev.out(N, fill=0x1234, rows=nt)
             o = ex.make_op(ex.GU_DN, case.bits, case.cb, dev.cls("gu"), dev.x, dev.sorted_tok, dev.off, y, nt,
                            case.top_k, dn=dn)
-            s = ex.alloc_scratch(o)
+            s = dev.scratch(o)
             print(f"launch_gather seed {seed} rep {rep} T {case.T} fused {fused}", flush=True)
             if fused:
-                assert ctr.numel() >= ex.ctr_bytes(o)
-                assert ex.launch_gather(o, s, ctr, wt, rt, out) == 0
+                assert ctr.n >= ex.ctr_bytes(o)
+                assert ex.launch_gather(o, s, ctr.view, wt, rt, out) == 0
             else:
                 assert ex.launch(o, s) == 0
                 assert ex.moe_gather(y, True, wt, rt, out) == 0
             torch.cuda.synchronize()
             ys.append(y.cpu().numpy().view(np.uint16))
             outs.append(out.cpu().numpy().view(np.uint16))
-        assert int(torch.count_nonzero(ctr)) == 0, "the counter block is not zero after the launch"
-        assert np.array_equal(ys[0], want_y) and np.array_equal(ys[1], want_y)
+        assert int(torch.count_nonzero(ctr.view)) == 0, "the counter block is not zero after the launch"
+        assert ctr.ok() and np.array_equal(ys[0], want_y) and np.array_equal(ys[1], want_y)
         assert np.array_equal(outs[0], outs[1])
         assert np.array_equal(outs[0], oracle.moe_gather(want_y, True, w, row_of, nt, top_k))
+
+
+def test_launch_gather_with_rows_past_t_leaves_the_counter_block_good(torch_cuda):
+    """row_of entries past T -- the scatter's rows of 80 pairs, the op launched over its first 70 -- name no row of
+    this launch: the fused gather counts a token's slots by the same predicate (0 <= row < T) as it sums them and as
+    its empty-token pass reads them, so every token completes and its counters return to zero. A second launch on the
+    same counter block (all 80 rows, in contract) then gives the bits of exl3c4_launch + exl3c4_moe_gather."""
+    import exl3c4 as ex
+    import oracle
+    torch = torch_cuda
+    case = Case(seed=87, n_tok=8, top_k=10, n_expert=96, geoms=[(512, 256)], bits=4, cb="mul1")
+    dev = Dev(case)
+    N = max(d["rows"] for d in dev.tabs["dn"])
+    _, _, _, row_of = oracle.moe_scatter_full(case.ids, case.n_expert)
+    rt = torch.from_numpy(row_of).cuda()
+    w = np.random.default_rng(88).random((case.n_tok, case.top_k)).astype(np.float32)
+    wt = torch.from_numpy(w).cuda()
+    ctr = dev.guard(1 << 16, fill=0)
+    T_short = 70
+    assert case.T == 80 and np.any(row_of >= T_short) and T_short >= ex.GD_FUSE_MIN_T
+    y = dev.out(N, rows=T_short)
+    out = dev.out(N, rows=case.n_tok)
+    o = dev.gd_op(y)
+    assert o.T == T_short
+    print(f"launch_gather over {T_short} of {case.T} rows", flush=True)
+    assert ex.launch_gather(o, dev.scratch(o), ctr.view, wt, rt, out) == 0
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(ctr.view)) == 0, "rows past T left counters behind"
+    print("launch_gather over all rows, same counter block", flush=True)
+    y2, out2 = dev.out(N), dev.out(N, rows=case.n_tok)
+    o2 = dev.gd_op(y2)
+    assert ex.launch_gather(o2, dev.scratch(o2), ctr.view, wt, rt, out2) == 0
+    y3, out3 = dev.out(N), dev.out(N, rows=case.n_tok)
+    o3 = dev.gd_op(y3)
+    assert ex.launch(o3, dev.scratch(o3)) == 0
+    assert ex.moe_gather(y3, True, wt, rt, out3) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y2, y3) and torch.equal(out2, out3)
+    assert int(torch.count_nonzero(ctr.view)) == 0
+    dev.check_guards("launch_gather with rows past T")
