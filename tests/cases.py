@@ -350,7 +350,7 @@ class Dev:
         rows = self.case.T if rows is None else rows
         g = self.guard(rows * cols * 2)
         v = g.view.view(self.torch.int16).view(rows, cols)
-        v.fill_(int(np.int16(np.uint16(fill).view(np.int16))))
+        v.fill_(int(np.uint16(fill & 0xFFFF).view(np.int16)))
         return v
 
     def prep(self, prefill=0xFFFF):
