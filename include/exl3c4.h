@@ -144,6 +144,19 @@ int exl3c4_launch_gather(const Exl3c4Op* op, void* scratch, int64_t scratch_byte
                          int64_t ctr_bytes, const float* expert_w, const int32_t* row_of, void* out,
                          int64_t out_pitch);
 
+/* THE LAUNCH THAT ALLOCATES NOTHING. No counterpart in the reference: for callers that cannot allocate or pass a
+ * workspace -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. exl3c4_launch_noalloc
+ * is exl3c4_launch (the same kernels, the same bits) with the library's own scratch: a file-scope device array of
+ * EXL3C4_NOALLOC_SCRATCH_BYTES, one on each GPU the library runs on, held until the process ends; the launch itself
+ * allocates nothing. A launch whose scratch (exl3c4_launch_scratch_bytes) exceeds it is refused with EXL3C4_E_SCRATCH
+ * before anything is written (at the configs' geometry -- gate/up 2048 -> 512, 512 experts -- that covers the decode
+ * band to M = 64 tokens of top-10 and small prefills). `stream` must belong to the current device (else
+ * EXL3C4_E_DEVICE). Every call on one GPU shares that GPU's array and leaves its contents behind: calls that may
+ * overlap on one GPU (two streams, two threads) race and must be ordered by the caller. */
+#define EXL3C4_NOALLOC_SCRATCH_BYTES (16ll << 20)
+int64_t exl3c4_noalloc_scratch_bytes(void);
+int     exl3c4_launch_noalloc(const Exl3c4Op* op, void* stream);
+
 /* The kernels a launch can run: prep_gu's rotation; gate_up's GEMM (with its input rotation), then for gate_up alone
  * its epilogue; down's GEMM with its epilogue (in gate_up_down it also forms h from gate_up's partial sums); and
  * gate_up_down's single kernel, which runs both GEMMs in one dispatch at decode once T >= EXL3C4_GD_FUSE_MIN_T.

@@ -59,6 +59,10 @@ def lib():
         L.exl3c4_scratch_bytes_geom.argtypes = [_i32, _i32, C.POINTER(_i32), C.POINTER(_i32), _i64, _i64, _i64]
         L.exl3c4_launch.restype = C.c_int
         L.exl3c4_launch.argtypes = [C.POINTER(Op), _p, _i64, _p]
+        L.exl3c4_launch_noalloc.restype = C.c_int
+        L.exl3c4_launch_noalloc.argtypes = [C.POINTER(Op), _p]
+        L.exl3c4_noalloc_scratch_bytes.restype = _i64
+        L.exl3c4_noalloc_scratch_bytes.argtypes = []
         L.exl3c4_launch_checked.restype = C.c_int
         L.exl3c4_launch_checked.argtypes = [C.POINTER(Op), _p, _i64, _p]
         L.exl3c4_dequant.restype = C.c_int
@@ -240,6 +244,11 @@ def launch(o: Op, scratch=None, stream=None) -> int:
     """Runs one op; returns the status (0 OK). `scratch`: a uint8 device tensor of >= scratch_bytes(o)."""
     n = 0 if scratch is None else scratch.numel()
     return int(lib().exl3c4_launch(C.byref(o), _ptr(scratch), n, _stream(stream)))
+
+
+def launch_noalloc(o: Op, stream=None) -> int:
+    """exl3c4_launch_noalloc: the launch in the library's own device scratch (no scratch argument, no allocation)."""
+    return int(lib().exl3c4_launch_noalloc(C.byref(o), _stream(stream)))
 
 
 def launch_checked(o: Op, scratch=None, stream=None) -> int:
