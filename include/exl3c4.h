@@ -245,6 +245,15 @@ int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64
  * the rest of the plane is left as it was. */
 int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes);
 
+/* ------------------------------------------------------------------ the plugin rows' instances (checkers' entries)
+ * The gate_up_down rows' init hooks return an instance holding a pool of counter blocks, one per (stream, output) pair,
+ * each with a host-visible flag the single decode kernel sets when a bounded wait gives up; the next launch on that
+ * block reports RAD_E_DEVICE. No counterpart in the reference's exports (its pool is internal): for tests and tools.
+ *   exl3c4_plugin_inst_flag          block's flag; when set >= 0 it is then written (a test forcing the failure path)
+ *   exl3c4_plugin_inst_blocks_used   the blocks handed out so far */
+int32_t exl3c4_plugin_inst_flag(void* inst, int32_t block, int32_t set);
+int32_t exl3c4_plugin_inst_blocks_used(void* inst);
+
 /* Library identity: "gfx950" and the ABI version above. */
 const char* exl3c4_build_target(void);
 int         exl3c4_abi_version(void);

@@ -12,7 +12,8 @@
 extern "C" {
 #endif
 
-/* Rows one MFMA row block holds: a chunk of an expert's run (the decode GEMV's unit of rows). */
+/* Rows one MFMA row block holds: the most a chunk of an expert's run holds on the decode path (the GEMV's unit of
+ * rows). A launch takes chunks of Exl3c4Launch.chunk_rows (a power of two up to this), its staged rows in LDS. */
 #define EXL3C4_CHUNK_ROWS 16
 /* Columns one wave's strip holds (two 16-column tiles) and k one step consumes (four 16-k tiles). */
 #define EXL3C4_STRIP 32
@@ -94,6 +95,7 @@ typedef struct Exl3c4Launch {
     int32_t        tail_from;     /* prefill GEMMs: nonzero asks for workgroups that zero the rows no run holds after
                                      the GEMM's (the launcher sets where they start) */
     int32_t        g_ntok;
+    int32_t        chunk_rows;    /* decode path: rows a chunk holds at most (a power of two <= EXL3C4_CHUNK_ROWS) */
 } Exl3c4Launch;
 #define EXL3C4_KERNARG_BYTES 632
 
@@ -112,6 +114,11 @@ int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 /* gate_up_down in one launch (k_gd): sync[0..T] zeroed first (exl3c4_dev_fill), then gate_up and down units */
 int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream);
+/* instance state (the plugin rows' init hooks): device memory zeroed once; pinned host memory the device writes */
+void* exl3c4_dev_zalloc(int64_t bytes);
+void  exl3c4_dev_free(void* p);
+void* exl3c4_host_zalloc(int64_t bytes);
+void  exl3c4_host_free(void* p);
 /* the prefill path */
 int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);
 int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1);

@@ -28,6 +28,7 @@
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
+#include <string.h>
 #include <utility>
 
 #include "exl3c4_dev.h"
@@ -301,21 +302,29 @@ __device__ __forceinline__ int perm_slot(int k) {
     return (k & ~15) | slot;
 }
 
-// The owner of sorted row i and its run, found by a whole workgroup at once: its 256 threads count the experts e in
-// [1, n_expert] with off[e] <= i (one round of independent loads), the counts meet in LDS, and the candidate is
-// checked against off[e] <= i < off[e + 1] (include/exl3_abi.h:136-141; -1 when no run holds the row). lo / hi: the
-// run clamped to [0, T) (kernels/exl3r4d/launch.c:14-15). Holds a barrier: every thread of the workgroup calls it.
+// The owner of sorted row i and its run (include/exl3_abi.h:136-141), found by a whole workgroup in ONE round of
+// independent loads: its threads read off[1 .. n_expert], count by wave ballots the e with off[e] <= i (for sorted
+// offsets, the owner's number) and keep the offsets in LDS, so the run's bounds off[e], off[e + 1] come from there
+// after the barrier instead of a second round of loads (up to OWNER_LDS experts; beyond, from memory). The row has an
+// owner when e < n_expert and off[e] <= i < off[e + 1]; else -1. lo / hi: the run clamped to [0, T)
+// (kernels/exl3r4d/launch.c:14-15). Holds a barrier: every thread of the workgroup calls it.
 struct Owner { int e, lo, hi; };
+constexpr int OWNER_LDS = 1024;
 __device__ Owner owner_wg(const Exl3c4Launch& a, int i) {
     __shared__ int cnt_s[4];
+    __shared__ int off_s[OWNER_LDS + 1];
+    const int n = a.n_expert, tid = (int)threadIdx.x;
     int cnt = 0;
-    for (int e = 1 + (int)threadIdx.x; e <= a.n_expert; e += 256) cnt += a.off[e] <= i ? 1 : 0;
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) cnt += __shfl_xor(cnt, d);
-    if ((threadIdx.x & 63) == 0) cnt_s[threadIdx.x >> 6] = cnt;
+    for (int e0 = 0; e0 <= n; e0 += 256) {                        // uniform trip count: ballots see every lane
+        const int e = e0 + tid;
+        const int o = e <= n ? a.off[e] : 0x7FFFFFFF;
+        if (e <= OWNER_LDS && e <= n) off_s[e] = o;
+        cnt += __popcll(__ballot(e >= 1 && o <= i));
+    }
+    if ((tid & 63) == 0) cnt_s[tid >> 6] = cnt;
     __syncthreads();
-    const int e = min(cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3], a.n_expert - 1);
-    const int o0 = a.off[e], o1 = a.off[e + 1];
+    const int e = min(cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3], n - 1);
+    const int o0 = e + 1 <= OWNER_LDS ? off_s[e] : a.off[e], o1 = e + 1 <= OWNER_LDS ? off_s[e + 1] : a.off[e + 1];
     Owner w;
     w.e = (o0 <= i && i < o1) ? e : -1;
     w.lo = max(o0, 0);
@@ -323,11 +332,17 @@ __device__ Owner owner_wg(const Exl3c4Launch& a, int i) {
     return w;
 }
 
-// A chunk is at most 16 rows of one run, cut from the run's first row: the workgroup keyed on the chunk's first row
-// does the chunk. Rows of the chunk: 0 when row i does not start one.
-__device__ __forceinline__ int chunk_rows(const Owner& w, int i) {
-    return (w.e >= 0 && ((i - w.lo) & (EXL3C4_CHUNK_ROWS - 1)) == 0) ? min(EXL3C4_CHUNK_ROWS, w.hi - i) : 0;
+// A chunk is at most a.chunk_rows rows of one run (a power of two), cut from the run's first row: the workgroup keyed
+// on the chunk's first row does the chunk. Rows of the chunk: 0 when row i does not start one. (Where the runs are
+// cut changes no bits: every row's products are its own MFMA row.)
+__device__ __forceinline__ int chunk_rows(const Exl3c4Launch& a, const Owner& w, int i) {
+    const int ch = a.chunk_rows;
+    return (w.e >= 0 && ((i - w.lo) & (ch - 1)) == 0) ? min(ch, w.hi - i) : 0;
 }
+
+// A lane's row of the staged chunk as the MFMA's A operand reads it: rows past the chunk's staged rows (whose
+// products are never written) read the last staged row, so no read leaves the workgroup's LDS.
+__device__ __forceinline__ int a_row(const Exl3c4Launch& a, int lane) { return min(lane & 15, a.chunk_rows - 1); }
 
 // f16(had128(f16(v * s))) over one 128-block, lane l holding k = l (0) and l + 64 (1) (kernels/exl3ref/ref.c:27-32).
 __device__ __forceinline__ void rotate_block(float f0, float f1, uint16_t s0, uint16_t s1, int lane, uint16_t& o0,
@@ -547,18 +562,29 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int S = a.ksplit;
     const int grp = u >> a.ksplit_log2, split = u & (S - 1);
+    // The start-up (owner, staging) runs at a raised wave priority, the GEMV loop at 0: a unit still starting when
+    // the others' loops run is not starved of issue slots, so gate_up's units finish together.
+    __builtin_amdgcn_s_setprio(2);
+    // the chunk's sorted_tok (lane q: row i + q), read beside the owner search (taken by readlane below)
+    const int tok_l = a.a_rot ? 0 : a.sorted[min(i + (lane & 15), a.T - 1)];
     const Owner w = owner_wg(a, i);
-    const int nrows = chunk_rows(w, i);
+    const int nrows = chunk_rows(a, w, i);
     if (!FUSED && u == 0 && threadIdx.x == 0) {
         a.row_info[2 * i] = w.e;
         a.row_info[2 * i + 1] = nrows;
     }
-    if (nrows == 0) return GuRows{ 0, w.e };
+    if (nrows == 0) {
+        __builtin_amdgcn_s_setprio(0);
+        return GuRows{ 0, w.e };
+    }
     const int c = class_of(a, w.e);
     const int64_t jx = entry_of(a, w.e);
     const Exl3c4DevClass& K = a.cls[c];
     const int N = K.rows, KC = K.cols;
-    if (grp * 128 >= N) return GuRows{ nrows, w.e };
+    if (grp * 128 >= N) {
+        __builtin_amdgcn_s_setprio(0);
+        return GuRows{ nrows, w.e };
+    }
     const int strip = grp * 4 + wave;
     const bool up = grp * 128 >= N / 2;
     const int nb = KC / 128, per = (nb + S - 1) / S;
@@ -567,35 +593,72 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     const gu32p rec = (gu32p)tab_entry(K.codes, K.codes_s, jx) +
                       ((int64_t)strip * (KC / EXL3C4_KSTEP) + 2 * b0) * 64 * BITS + lane * BITS;
     CodeRing<BITS> ring;
-    prime<BITS>(rec, ksn, ring);                                  // its first steps' words fly during the staging
 
-    uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
+    uint16_t* A = (uint16_t*)lds;                                 // [chunk_rows][kp]
     const void* sv = up ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx);
-    for (int q = 0; q < nrows; ++q) {
-        const int64_t r = i + q;
-        const int tok = a.a_rot ? 0 : a.sorted[r];
-        int64_t src = a.a_rot ? r : tok / a.top_k;
-        src = src < a.x_rows ? src : a.x_rows - 1;
-        for (int hb = b0 + wave; hb < b1; hb += 4) {
-            uint16_t v0 = 0, v1 = 0;
-            if (a.a_rot) {
-                const void* xs = (const uint16_t*)a.x + src * a.x_pitch + (up ? KC : 0) + hb * 128;
-                v0 = ldg16(xs, lane);
-                v1 = ldg16(xs, lane + 64);
-            } else if (tok >= 0) {
-                const void* xs = (const uint16_t*)a.x + src * a.x_pitch + hb * 128;
-                const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
-                const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
-                const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
-                rotate_block(f0, f1, ldg16(sv, hb * 128 + lane), ldg16(sv, hb * 128 + 64 + lane), lane, v0, v1);
+    // The wave's 128-blocks hb = b0 + wave + 4 j of the split: up to GU_WB of them have their scale and input loads
+    // issued together, a row at a time, before any rotation (one memory round trip a row, not one a block); the
+    // addresses of blocks past the split are clamped (loaded, unused). Wider splits take the rest one at a time.
+    constexpr int GU_WB = 4;
+    const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
+    if (ksn > 0) {
+        int hbj[GU_WB];
+        uint16_t s0[GU_WB], s1[GU_WB];
+#pragma unroll
+        for (int j = 0; j < GU_WB; ++j) {
+            hbj[j] = min(b0 + wave + 4 * j, b1 - 1);
+            s0[j] = a.a_rot ? 0 : ldg16(sv, hbj[j] * 128 + lane);
+            s1[j] = a.a_rot ? 0 : ldg16(sv, hbj[j] * 128 + 64 + lane);
+        }
+        for (int q = 0; q < nrows; ++q) {
+            const int64_t r = i + q;
+            const int tok = a.a_rot ? 0 : __builtin_amdgcn_readlane(tok_l, q);
+            int64_t src = a.a_rot ? r : (tok >= 0 ? tok / a.top_k : 0);
+            src = src < a.x_rows ? src : a.x_rows - 1;
+            const uint16_t* xr = (const uint16_t*)a.x + src * a.x_pitch + (a.a_rot && up ? KC : 0);
+            uint16_t x0[GU_WB], x1[GU_WB];
+#pragma unroll
+            for (int j = 0; j < GU_WB; ++j) {
+                x0[j] = ldg16(xr, hbj[j] * 128 + lane);
+                x1[j] = ldg16(xr, hbj[j] * 128 + 64 + lane);
             }
-            lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
+            // the codes' first steps go out behind the first row's input (loads complete in order: the staging
+            // waits for its own loads only) and fly during the rotation
+            if (q == 0) prime<BITS>(rec, ksn, ring);
+#pragma unroll
+            for (int j = 0; j < GU_WB; ++j) {
+                if (j >= nbw) break;
+                uint16_t v0 = 0, v1 = 0;
+                if (a.a_rot) {
+                    v0 = x0[j];
+                    v1 = x1[j];
+                } else if (tok >= 0) {
+                    const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0[j]) : h2f(x0[j]);
+                    const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1[j]) : h2f(x1[j]);
+                    rotate_block(f0, f1, s0[j], s1[j], lane, v0, v1);
+                }
+                lds_put(A, q, kp, (hbj[j] - b0) * 128, lane, v0, v1);
+            }
+            for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
+                uint16_t v0 = 0, v1 = 0;
+                const uint16_t y0 = ldg16(xr, hb * 128 + lane), y1 = ldg16(xr, hb * 128 + 64 + lane);
+                if (a.a_rot) {
+                    v0 = y0;
+                    v1 = y1;
+                } else if (tok >= 0) {
+                    const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(y0) : h2f(y0);
+                    const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(y1) : h2f(y1);
+                    rotate_block(f0, f1, ldg16(sv, hb * 128 + lane), ldg16(sv, hb * 128 + 64 + lane), lane, v0, v1);
+                }
+                lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
+            }
         }
     }
     __syncthreads();
+    __builtin_amdgcn_s_setprio(0);
 
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    gemv_strip<BITS, CB>(rec, ksn, ring, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
+    gemv_strip<BITS, CB>(rec, ksn, ring, A + a_row(a, lane) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // D lane l: column l % 16 (c' = 2 s + t -> weight row 32 nb + 16 t + s, + 8 for acc1), rows 4 (l / 16) + 0..3
     const int cc = lane & 15, rg = lane >> 4;
@@ -785,6 +848,7 @@ __device__ __forceinline__ DnW dn_weight(bool gd, const Exl3c4DevClass& K) {
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __builtin_amdgcn_s_setprio(2);                                // the start-up at a raised priority (gu_unit)
     int e, nrows;
     if (!FUSED && a.row_info) {
         e = a.row_info[2 * i];
@@ -792,7 +856,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     } else {
         const Owner w = owner_wg(a, i);
         e = w.e;
-        nrows = chunk_rows(w, i);
+        nrows = chunk_rows(a, w, i);
     }
     if (e < 0) {
         if (wave == 0) {
@@ -814,8 +878,8 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         return;
     }
     const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
-    uint16_t* A = (uint16_t*)lds;                                 // [16][kp]
-    float* acc_l = (float*)lds;                                   // [16][128], over A once every wave is done with it
+    uint16_t* A = (uint16_t*)lds;                                 // [chunk_rows][kp]
+    float* acc_l = (float*)lds;                                   // [chunk_rows][128], over A once the waves are done
 
     // this wave's strip of the block, all of k; its first codes are in flight while the rows are staged
     const int strip = 4 * b + wave;
@@ -841,7 +905,22 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
 
     // stage the chunk's rows
     const int nhb = KC / 128;
-    for (int q = 0; q < nrows; ++q) {
+    if (FUSED && nhb <= 4) {                                      // each wave one block of h: every row's loads first
+        constexpr int R = EXL3C4_CHUNK_ROWS;
+        const int hb = wave;
+        uint16_t h0[R], h1[R];
+#pragma unroll
+        for (int q = 0; q < R; ++q) {
+            const uint16_t* hs = a.hbuf + (int64_t)(i + min(q, nrows - 1)) * a.hbuf_pitch + min(hb, nhb - 1) * 128;
+            if (q < a.chunk_rows) {
+                h0[q] = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                h1[q] = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < R; ++q)
+            if (q < nrows && hb < nhb) lds_put(A, q, kp, hb * 128, lane, h0[q], h1[q]);
+    } else for (int q = 0; q < nrows; ++q) {
         const int64_t r = i + q;
         for (int hb = wave; hb < nhb; hb += 4) {
             uint16_t v0 = 0, v1 = 0;
@@ -867,8 +946,9 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     }
     __syncthreads();
 
+    __builtin_amdgcn_s_setprio(0);
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
-    gemv_strip<BITS, CB>(rec, ksteps, ring, A + (lane & 15) * kp + 16 * (lane >> 4), acc0, acc1);
+    gemv_strip<BITS, CB>(rec, ksteps, ring, A + a_row(a, lane) * kp + 16 * (lane >> 4), acc0, acc1);
 
     // the block's accumulations to LDS (column of D lane l: 16 (l & 1) + (l / 2) within the strip, + 8 for acc1)
     __syncthreads();
@@ -911,6 +991,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
 // from the rows' partial sums, once, by the row's last gate_up unit: into hbuf, then one more count on row i's counter.
 __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows& g) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __builtin_amdgcn_s_setprio(2);                                // every down unit of the row waits for this
     const int c = class_of(a, g.e);
     const int64_t jx = entry_of(a, g.e);
     const Exl3c4DevClass& G = a.cls[c];
@@ -927,6 +1008,7 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, i), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_setprio(0);
 }
 
 // gate_up_down in one launch (decode path). Workgroups g = 8 k + x (x < 8) take the sorted rows i = x (mod 8): first
@@ -1605,9 +1687,10 @@ int go2(F f, dim3 grid, hipStream_t s, void* ev0, void* ev1, uint32_t lds, Args.
     return hipGetLastError() == hipSuccess ? 0 : EXL3C4_E_DEVICE;
 }
 
-// down's LDS: the staged rows [16][lds_pitch] halves, later the block's accumulations [16][128] f32 over them
+// down's LDS: the staged rows [chunk_rows][lds_pitch] halves, later the block's accumulations [chunk_rows][128] f32
+// over them
 uint32_t dn_lds_bytes(const Exl3c4Launch* a) {
-    const uint32_t rows = (uint32_t)(16 * a->lds_pitch * 2), acc = 16 * 128 * 4;
+    const uint32_t rows = (uint32_t)(a->chunk_rows * a->lds_pitch * 2), acc = (uint32_t)(a->chunk_rows * 128 * 4);
     return rows > acc ? rows : acc;
 }
 
@@ -1623,7 +1706,7 @@ extern "C" int exl3c4_dev_gu(const Exl3c4Launch* a, void* stream, void* ev0, voi
     const GemmFn f = by_bits<GuK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->T <= 0 || a->n_grp <= 0) return 0;
-    const uint32_t lds = (uint32_t)(16 * a->lds_pitch * 2);
+    const uint32_t lds = (uint32_t)(a->chunk_rows * a->lds_pitch * 2);
     return go2(f, dim3((unsigned)(a->n_grp * a->ksplit), (unsigned)a->T), (hipStream_t)stream, ev0, ev1, lds, *a);
 }
 
@@ -1645,10 +1728,34 @@ extern "C" int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, voi
     const GemmFn f = by_bits<GdK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->T <= 0 || a->n_grp <= 0 || a->nblk <= 0) return 0;
-    const uint32_t gu_lds = (uint32_t)(16 * a->lds_pitch_gu * 2), dn_lds = dn_lds_bytes(a);
+    const uint32_t gu_lds = (uint32_t)(a->chunk_rows * a->lds_pitch_gu * 2), dn_lds = dn_lds_bytes(a);
     const int64_t per_xcd = (int64_t)((a->T + 7) / 8) * (((int64_t)a->n_grp << a->ksplit_log2) + a->nblk) +
                             (a->g_out ? (a->g_ntok + 31) / 32 : 0);  /* gather_empty: 4 tokens a workgroup */
     return go2(f, dim3((unsigned)(8 * per_xcd)), (hipStream_t)stream, ev0, ev1, gu_lds > dn_lds ? gu_lds : dn_lds, *a);
+}
+
+// Instance state of the plugin rows (what a row's init hook allocates, never a launch): device memory zeroed once,
+// and pinned host memory the device can write (a flag the host reads without a synchronisation).
+extern "C" void* exl3c4_dev_zalloc(int64_t bytes) {
+    void* p = nullptr;
+    if (bytes <= 0 || hipMalloc(&p, (size_t)bytes) != hipSuccess) return nullptr;
+    if (hipMemset(p, 0, (size_t)bytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    return p;
+}
+extern "C" void exl3c4_dev_free(void* p) {
+    if (p) (void)hipFree(p);
+}
+extern "C" void* exl3c4_host_zalloc(int64_t bytes) {
+    void* p = nullptr;
+    if (bytes <= 0 || hipHostMalloc(&p, (size_t)bytes, hipHostMallocCoherent) != hipSuccess) return nullptr;
+    memset(p, 0, (size_t)bytes);
+    return p;
+}
+extern "C" void exl3c4_host_free(void* p) {
+    if (p) (void)hipHostFree(p);
 }
 
 extern "C" int exl3c4_dev_fill(int32_t* p, int64_t n, void* stream) {

@@ -38,20 +38,37 @@ static int64_t max_rows(const Exl3c4Op* o) {
     return m;
 }
 
-/* Chunks of at most 16 rows the runs of T sorted rows can make over n_expert experts. */
-static int64_t chunk_bound(int64_t T, int64_t n_expert) {
-    return T / EXL3C4_CHUNK_ROWS + (n_expert < T ? n_expert : T) + 1;
+/* Rows a decode-path chunk holds at most: the least power of two >= min(M, 16). A token's top_k experts are distinct,
+ * so an expert's run in a batch of M tokens holds at most M rows, and a chunk stages no more rows than a run can have
+ * (at decode, M = 8: half the LDS of 16-row chunks). A routing that repeats an expert within a token makes longer runs;
+ * they are cut into more chunks, with the same bits. */
+static int chunk_for(int64_t M) {
+    int c = 1;
+    while (c < EXL3C4_CHUNK_ROWS && c < M) c <<= 1;
+    return c;
 }
 
-/* Split-K of one GEMV launch, from the geometry alone (never the routing, so a row's bits do not depend on the batch):
- * enough waves to fill the device, at most 16 splits and never more than the k steps. */
-#ifndef EXL3C4_TARGET_WAVES
-#define EXL3C4_TARGET_WAVES 8192
+/* Chunks of at most ch rows the runs of T sorted rows can make over n_expert experts. */
+static int64_t chunk_bound(int64_t T, int64_t n_expert, int ch) {
+    return T / ch + (n_expert < T ? n_expert : T) + 1;
+}
+
+/* gate_up's split-K on the decode path, from T, M and the geometry (never the routing): the most splits -- a power of
+ * two, at most 16 and at most one a 128-block of k -- that still leave every gate_up unit of the launch resident at
+ * once (GU_SLOTS workgroups: 256 CUs x 7), so that gate_up_down's single kernel runs all of gate_up as one phase at
+ * full occupancy and every row's down units follow it, with no late round of gate_up units whose down units would
+ * run after it alone; then more splits while a split's staged rows would take more LDS than GU_LDS_BUDGET (which
+ * keeps 7 workgroups a CU). */
+#ifndef GU_SLOTS
+#define GU_SLOTS 1792
 #endif
-static int ksplit_for(int64_t chunks, int64_t strips, int64_t ksteps) {
-    const int64_t units = chunks * strips;
+#ifndef GU_LDS_BUDGET
+#define GU_LDS_BUDGET (20 * 1024)
+#endif
+static int ksplit_for(int64_t chunks, int64_t n_grp, int64_t nb_min, int64_t nb_max, int ch) {
     int s = 1;
-    while (s < 16 && 2 * s <= ksteps && units * s < EXL3C4_TARGET_WAVES) s *= 2;   /* a power of two */
+    while (s < 16 && 2 * s <= nb_min && chunks * n_grp * 2 * s <= GU_SLOTS) s *= 2;
+    while (s < 16 && 2 * s <= nb_max && (int64_t)ch * (((nb_max + s - 1) / s) * 128 + 8) * 2 > GU_LDS_BUDGET) s *= 2;
     return s;
 }
 
@@ -91,7 +108,7 @@ typedef struct Carve {
     int     h_gepi;                               /* gate_up_down, decode path below that (GEPI_ROWS): h by k_gepi */
     int64_t row_info, plan, xr, part, h, dacc, sync, total;
     int64_t T, part_pitch, dacc_pitch, xr_pitch, h_pitch, max_chunks;
-    int     split_gu, gu_lds_pitch, dn_lds_pitch;
+    int     split_gu, gu_lds_pitch, dn_lds_pitch, chunk;
 } Carve;
 
 /* The scratch of one launch with T sorted rows, each region 256-B aligned.
@@ -105,6 +122,7 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     memset(k, 0, sizeof *k);
     k->T = T;
     k->pf = prefill_path(o, T);
+    k->chunk = chunk_for(o->M);
     int64_t off = 0;
     const int gu = op == EXL3C4_GATE_UP || op == EXL3C4_GU_DN;
     const int dn = op == EXL3C4_DOWN || op == EXL3C4_GU_DN;
@@ -130,9 +148,8 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
             if (nb > nb_max) nb_max = nb;
         }
         int s = 1;
-        if (!k->pf) {   /* split-K: from T and the geometry; at most 12 128-blocks of k a split, so rows fit LDS */
-            s = ksplit_for(chunk_bound(T, o->n_expert), rc / EXL3C4_STRIP, 2 * nb_min);
-            while ((nb_max + s - 1) / s > 12) s *= 2;
+        if (!k->pf) {   /* split-K from T, M and the geometry: ksplit_for */
+            s = ksplit_for(chunk_bound(T, o->n_expert, k->chunk), rc / 128, nb_min, nb_max, k->chunk);
             k->gu_lds_pitch = (int)(((nb_max + s - 1) / s) * 128 + 8);
         }
         k->split_gu = s;
@@ -355,6 +372,7 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->y_pitch = (int32_t)o->y_pitch;
     a->y_cols = (int32_t)o->y_cols;
     a->blk_per_wave = 1;
+    a->chunk_rows = k->chunk;
 }
 
 /* How a launch runs: the events of a timed launch go to exactly one kernel of the sequence; keep_sums has the

@@ -12,10 +12,13 @@
  *     (include/exl3_abi.h:751-800);
  *   - the plane extents of a table entry (include/exl3_abi.h:647-665) and the class interleave (:847-853).
  * Operand positions are not tabulated: each is found by its name in the schema (codes, codes_odd, codes_1, ...). */
+#include <pthread.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "exl3c4.h"
+#include "exl3c4_dev.h"
 #include "rad_shim.h"
 
 /* the stored form of a codes table entry (exl3c4_relayout's record), as an element type of its own */
@@ -367,12 +370,123 @@ static int build_op(const RadArgs* a, int si, Exl3c4Op* o) {
     return RAD_OK;
 }
 
+/* ------------------------------------------------------------------ instance state: the counter blocks
+ *
+ * gate_up_down's single decode kernel orders its workgroups through a counter block that is zero when it starts and
+ * that a good launch leaves zero. The gate_up_down rows' instances (RadKernelInfo::init: once per resolved instance,
+ * never on the launch path) hold a pool of CTR_BLOCKS such blocks, allocated and zeroed at init, one taken per
+ * (stream, output) pair on first use under a mutex: two launches that may overlap run on two streams or write two
+ * outputs, so they never share a block, and two that share one are ordered on its stream (the reference's pool,
+ * kernels/exl3r4d/launch.c:311-330, 464-500). A launch past the pool, or with no instance (a tool calling the hook
+ * cold), runs exl3c4_launch, which zeroes counters in its scratch with one more dispatch: the same bits.
+ *
+ * Each block has a flag in pinned host memory that the kernel sets when one of its bounded waits gives up (the launch's
+ * output is then void). The host reads it without a synchronisation: the next launch that takes the block finds it
+ * set, re-zeroes the block on its stream, clears the flag and returns RAD_E_DEVICE before writing anything; the launch
+ * after that runs normally. */
+#define CTR_BLOCKS 16
+#define FLAG_STRIDE 16                                 /* int32s between two blocks' flags (a 64-byte line each) */
+
+typedef struct Inst {
+    int32_t*        ctr;                               /* CTR_BLOCKS blocks of block_bytes, zeroed at init */
+    int64_t         block_bytes;
+    int32_t*        fail;                              /* pinned host flags, FLAG_STRIDE apart */
+    int             used;
+    RadStream       key_s[CTR_BLOCKS];
+    const void*     key_o[CTR_BLOCKS];
+    pthread_mutex_t mu;
+} Inst;
+
+/* Counter-block bytes of gate_up_down at a band of M tokens: the status word and a counter a sorted row, then a line a
+ * token (exl3c4_ctr_bytes' layout), 256 B apart. */
+static int64_t ctr_block_bytes(int64_t M, int64_t top_k) {
+    return ((M * top_k + 1 + M) * EXL3C4_SYNC_STRIDE * 4 + 255) / 256 * 256;
+}
+
+static int inst_init(const RadParam* p, int n_p, int si, void** out) {
+    Geom g;
+    *out = NULL;
+    const int two = !mod4_of(si) && (rad_param_find(p, n_p, "N_odd") || rad_param_find(p, n_p, "K_odd"));
+    if (geom(p, n_p, si, two, &g) != RAD_OK) return RAD_OK;   /* the launch refuses the geometry itself */
+    Inst* q = (Inst*)calloc(1, sizeof *q);
+    if (!q) return RAD_OK;                             /* no instance: every launch zeroes its own counters */
+    q->block_bytes = ctr_block_bytes(g.M, g.top_k);
+    q->ctr = (int32_t*)exl3c4_dev_zalloc(q->block_bytes * CTR_BLOCKS);
+    q->fail = (int32_t*)exl3c4_host_zalloc((int64_t)CTR_BLOCKS * FLAG_STRIDE * 4);
+    if (!q->ctr || !q->fail) {
+        exl3c4_dev_free(q->ctr);
+        exl3c4_host_free(q->fail);
+        free(q);
+        return RAD_OK;
+    }
+    pthread_mutex_init(&q->mu, NULL);
+    *out = q;
+    return RAD_OK;
+}
+
+static void inst_fini(void* inst) {
+    Inst* q = (Inst*)inst;
+    if (!q) return;
+    exl3c4_dev_free(q->ctr);
+    exl3c4_host_free(q->fail);
+    pthread_mutex_destroy(&q->mu);
+    free(q);
+}
+
+/* This launch's block (host bookkeeping only), or -1: past the pool. */
+static int block_of(Inst* q, RadStream s, const void* out) {
+    int b = -1;
+    pthread_mutex_lock(&q->mu);
+    for (int i = 0; i < q->used && b < 0; ++i)
+        if (q->key_s[i] == s && q->key_o[i] == out) b = i;
+    if (b < 0 && q->used < CTR_BLOCKS) {
+        b = q->used++;
+        q->key_s[b] = s;
+        q->key_o[b] = out;
+    }
+    pthread_mutex_unlock(&q->mu);
+    return b;
+}
+
+int32_t exl3c4_plugin_inst_flag(void* inst, int32_t block, int32_t set) {
+    Inst* q = (Inst*)inst;
+    if (!q || block < 0 || block >= CTR_BLOCKS) return -1;
+    volatile int32_t* f = q->fail + (int64_t)block * FLAG_STRIDE;
+    const int32_t v = *f;
+    if (set >= 0) *f = set;
+    return v;
+}
+
+int32_t exl3c4_plugin_inst_blocks_used(void* inst) {
+    Inst* q = (Inst*)inst;
+    if (!q) return -1;
+    pthread_mutex_lock(&q->mu);
+    const int n = q->used;
+    pthread_mutex_unlock(&q->mu);
+    return n;
+}
+
 /* ------------------------------------------------------------------ hooks */
 
 static int launch_si(const RadArgs* a, RadStream s, int si) {
     Exl3c4Op o;
     const int rc = build_op(a, si, &o);
-    return rc != RAD_OK ? rc : exl3c4_launch(&o, a->scratch, a->scratch_bytes, s);
+    if (rc != RAD_OK) return rc;
+    Inst* q = (Inst*)a->inst;
+    if (q && o.op == EXL3C4_GU_DN && (o.T + 1 + o.M) * EXL3C4_SYNC_STRIDE * 4 <= q->block_bytes) {
+        const int b = block_of(q, s, o.y);
+        if (b >= 0) {
+            int32_t* blk = q->ctr + b * (q->block_bytes / 4);
+            volatile int32_t* f = q->fail + (int64_t)b * FLAG_STRIDE;
+            if (*f) {                                  /* the block's last launch gave up a wait: its output was void */
+                *f = 0;
+                const int zr = exl3c4_dev_fill(blk, q->block_bytes / 4, s);
+                return zr != 0 ? zr : RAD_E_DEVICE;
+            }
+            return exl3c4_launch_inst(&o, a->scratch, a->scratch_bytes, s, blk, q->block_bytes, (int32_t*)f);
+        }
+    }
+    return exl3c4_launch(&o, a->scratch, a->scratch_bytes, s);
 }
 /* from the parameters alone, at the band top (docs/STEP0.md:142-146) */
 static int64_t scratch_si(const RadArgs* a, int si) {
@@ -554,6 +668,9 @@ HOOKS(5, dn4)
 HOOKS(6, pg4)
 HOOKS(7, gd4)
 #undef HOOKS
+/* the gate_up_down rows' instances: a counter-block pool (rank and world are not read: one GPU's instance) */
+static int gd_init(const RadParam* p, int n_p, int rank, int world, void** out) { return inst_init(p, n_p, 3, out); }
+static int gd4_init(const RadParam* p, int n_p, int rank, int world, void** out) { return inst_init(p, n_p, 7, out); }
 
 /* ------------------------------------------------------------------ rows */
 
@@ -575,11 +692,12 @@ static const RadConstraint c_gd[] = {   /* down's k is N / 2 */
     RAD_CDIV("K", 128), RAD_CDIV("N", 256), RAD_CLE("N", 3072), RAD_CLE("n_expert", 65536),
 };
 
-#define ROW(nm, opname, c, what, shp, dts)                                                                         \
+#define ROW_I(nm, opname, c, what, shp, dts, ini, fin)                                                            \
     { .name = "exl3c4_" #nm, .op = (opname), .family = "moe", .computes = (what), .shape = (shp), .dtypes = (dts),     \
       .domain = RAD_DOMAIN_DEVICE, .priority = 10, .constraints = (c), .n_constraints = N_OF(c),                   \
-      .init = NULL, .fini = NULL, .launch = nm##_launch, .scratch = nm##_scratch, .layout = nm##_layout,           \
+      .init = (ini), .fini = (fin), .launch = nm##_launch, .scratch = nm##_scratch, .layout = nm##_layout,         \
       .relayout = nm##_relayout, .opd_shape = nm##_shape, .unrelayout = nm##_unrelayout }
+#define ROW(nm, opname, c, what, shp, dts) ROW_I(nm, opname, c, what, shp, dts, NULL, NULL)
 
 static const RadKernelInfo k_rows[8] = {   /* row i serves schema i */
     ROW(gu, "moe_exl3_gate_up", c_gu, "gate and up, f16 h: input rotation staged in LDS, trellis decode in registers into "
@@ -588,15 +706,18 @@ static const RadKernelInfo k_rows[8] = {   /* row i serves schema i */
     ROW(dn, "moe_exl3_down", c_dn, "down, bf16 y: input staged (rotated) in LDS, trellis decode into MFMA, output rotation in the "
         "workgroup", "K % 128 and K <= 1536, N % 128", DTYPES ", " CODEBOOKS "; h f16; y bf16"),
     ROW(pg, "moe_exl3_prep_gu", c_pg, "gate_up's input rotation as an op", "K % 128", DTYPES "; a f16 or bf16; xr f16"),
-    ROW(gd, "moe_exl3_gate_up_down", c_gd, "the decode chain as one op: gate_up's GEMM, then down's with h built from gate_up's partial "
-        "sums in LDS (two launches)", "K % 128, N % 256 and N <= 3072", DTYPES ", " CODEBOOKS "; a f16 or bf16; y bf16"),
+    ROW_I(gd, "moe_exl3_gate_up_down", c_gd, "the decode chain as one op: from 32 sorted rows both GEMMs in one kernel (down "
+          "units wait on their rows' counters, in the instance's counter block), below it gate_up's GEMM then down's; "
+          "the prefill path's two expert-grouped GEMMs from 8 rows an expert", "K % 128, N % 256 and N <= 3072",
+          DTYPES ", " CODEBOOKS "; a f16 or bf16; y bf16", gd_init, inst_fini),
     ROW(gu4, "moe_exl3_gate_up_mod4", c_gu, "gate and up over four classes by expert number mod 4", "K % 128, N % 256",
         DTYPES ", " CODEBOOKS "; a f16 or bf16; h f16"),
     ROW(dn4, "moe_exl3_down_mod4", c_dn, "down over four classes by expert number mod 4", "K % 128 and K <= 1536, N % 128",
         DTYPES ", " CODEBOOKS "; h f16; y bf16"),
     ROW(pg4, "moe_exl3_prep_gu_mod4", c_pg, "gate_up's input rotation over four classes", "K % 128", DTYPES "; a f16 or bf16; xr f16"),
-    ROW(gd4, "moe_exl3_gate_up_down_mod4", c_gd, "the decode chain over four classes", "K % 128, N % 256 and N <= 3072",
-        DTYPES ", " CODEBOOKS "; a f16 or bf16; y bf16"),
+    ROW_I(gd4, "moe_exl3_gate_up_down_mod4", c_gd, "the decode chain over four classes (one kernel from 32 sorted rows, "
+          "the instance's counter block)", "K % 128, N % 256 and N <= 3072", DTYPES ", " CODEBOOKS "; a f16 or bf16; y bf16",
+          gd4_init, inst_fini),
 };
 #undef ROW
 
@@ -615,5 +736,6 @@ int                  rad_kernel_schema_count(void) { return 8; }
 const RadOpSchema*   rad_kernel_schema_at(int i) { return i >= 0 && i < 8 ? &k_schema[i] : NULL; }
 int                  rad_kernel_count(void) { return 8; }
 const RadKernelInfo* rad_kernel_at(int i) { return i >= 0 && i < 8 ? &k_rows[i] : NULL; }
-/* A launch reads and writes its operands and its scratch slice only: no counters, no globals, nothing kept. */
+/* A launch reads and writes its operands, its scratch slice and (gate_up_down) its instance's counter block for its
+ * (stream, output) pair only, so launches the engine overlaps never share state. */
 int rad_kernel_concurrent(int i) { return i >= 0 && i < 8; }

@@ -73,6 +73,8 @@ class Constraint(C.Structure):
     _fields_ = [("key", C.c_char_p), ("kind", C.c_int), ("v", C.c_int64), ("set", C.c_char_p)]
 
 
+INIT = C.CFUNCTYPE(C.c_int, C.POINTER(Param), C.c_int, C.c_int, C.c_int, C.POINTER(C.c_void_p))
+FINI = C.CFUNCTYPE(None, C.c_void_p)
 LAUNCH = C.CFUNCTYPE(C.c_int, C.POINTER(Args), C.c_void_p)
 SCRATCH = C.CFUNCTYPE(C.c_int64, C.POINTER(Args))
 SHAPE = C.CFUNCTYPE(C.c_int, C.POINTER(Param), C.c_int, C.c_int, C.POINTER(OpdDesc))
@@ -88,7 +90,7 @@ class KernelInfo(C.Structure):
     _fields_ = [("name", C.c_char_p), ("op", C.c_char_p), ("family", C.c_char_p), ("computes", C.c_char_p),
                 ("shape", C.c_char_p), ("dtypes", C.c_char_p), ("domain", C.c_int), ("priority", C.c_int),
                 ("constraints", C.POINTER(Constraint)), ("n_constraints", C.c_int),
-                ("init", C.c_void_p), ("fini", C.c_void_p), ("launch", LAUNCH), ("scratch", SCRATCH),
+                ("init", INIT), ("fini", FINI), ("launch", LAUNCH), ("scratch", SCRATCH),
                 ("layout", LAYOUT), ("relayout", RELAYOUT), ("opd_shape", SHAPE), ("unrelayout", UNRELAYOUT)]
 
 
@@ -107,6 +109,10 @@ def bind(lib):
     lib.rad_kernel_at.restype = C.POINTER(KernelInfo)
     lib.rad_kernel_at.argtypes = [C.c_int]
     lib.rad_kernel_concurrent.argtypes = [C.c_int]
+    lib.exl3c4_plugin_inst_flag.restype = C.c_int32
+    lib.exl3c4_plugin_inst_flag.argtypes = [C.c_void_p, C.c_int32, C.c_int32]
+    lib.exl3c4_plugin_inst_blocks_used.restype = C.c_int32
+    lib.exl3c4_plugin_inst_blocks_used.argtypes = [C.c_void_p]
     lib.exl3c4_scratch_bytes_geom.restype = C.c_int64
     lib.exl3c4_scratch_bytes_geom.argtypes = [C.c_int32, C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                               C.c_int64, C.c_int64, C.c_int64]

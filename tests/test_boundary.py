@@ -83,10 +83,12 @@ def test_band_top_scratch_takes_every_smaller_batch(which, H, W, E, M, top_k):
 
 
 def test_the_carve_is_not_monotone_so_the_band_top_alone_would_not_do():
-    """Why the maximum is needed (the control): at configs[2] a batch of 50 rows needs more than one of 80."""
-    n50 = exl3c4.launch_scratch_bytes(op(exl3c4.GU_DN, H=2048, W=512, E=512, M=8, top_k=10, rows_T=50))
-    n80 = exl3c4.launch_scratch_bytes(op(exl3c4.GU_DN, H=2048, W=512, E=512, M=8, top_k=10, rows_T=80))
-    assert n50 > n80
+    """Why the maximum is needed (the control): one expert with a band of 64 tokens -- 64 rows take the prefill path,
+    63 the decode path, whose partial sums at its split-K need more than three times the band top's carve."""
+    n63 = exl3c4.launch_scratch_bytes(op(exl3c4.GU_DN, H=2048, W=512, E=1, M=64, top_k=1, rows_T=63))
+    n64 = exl3c4.launch_scratch_bytes(op(exl3c4.GU_DN, H=2048, W=512, E=1, M=64, top_k=1, rows_T=64))
+    assert n63 > 3 * n64
+    assert exl3c4.scratch_bytes(op(exl3c4.GU_DN, H=2048, W=512, E=1, M=64, top_k=1)) >= n63
 
 
 @pytest.mark.parametrize("which,a_rot", [(exl3c4.DOWN, 0), (exl3c4.GATE_UP, 1)])

@@ -1,6 +1,9 @@
 """Launches through the radiance plugin rows of libexl3c4.so (RadArgs built as an engine would: operands in schema order,
-stacked weight tables, params) give the same bits as the C-ABI entry points (exl3c4_launch), for every op, two-class
-and four-class."""
+weight tables, params) give the same bits as the C-ABI entry points (exl3c4_launch), for every op, two-class and
+four-class, with the tables in both of the engine's forms: stacked buffers, and pointer tables (stride 0: entry j at
+((void**)base)[j], what the engine hands over). The gate_up_down rows' instances (init / fini: a counter-block pool)
+give the same bits, keep their blocks zero, and report a wait that gave up as RAD_E_DEVICE on the block's next
+launch."""
 import ctypes as C
 import json
 import os
@@ -63,8 +66,20 @@ class Plug:
         g.update(extra)
         return rp.Params(**g)
 
-    def run(self, si, x, y, ydt, **extra):
-        """Launch row si with input tensor x (torch) and output y (torch int16); returns the status."""
+    def _ptr_table(self, t, dtype, ext):
+        """The engine's form of a stacked table t [E, ...]: a device array of E entry addresses, stride 0."""
+        torch = self.dev.torch
+        step = t.stride(0) * t.element_size()
+        addrs = torch.tensor([t.data_ptr() + j * step for j in range(t.shape[0])], dtype=torch.int64, device="cuda")
+        self._keep.append(addrs)
+        shape = [t.shape[0]] + list(ext)
+        return rp.tensor(addrs.data_ptr(), dtype, shape, [0] + [int(np.prod(ext[1:])) if len(ext) > 1 else 1] +
+                         ([1] if len(ext) > 1 else []))
+
+    def run(self, si, x, y, ydt, ptr=False, inst=None, **extra):
+        """Launch row si with input tensor x (torch) and output y (torch int16); returns the status. ptr: every weight
+        table as a pointer table; inst: the row instance to hand over (RadArgs.inst)."""
+        self._keep = []
         c = self.case
         schema = TABLES["schemas"][si]
         pos = TABLES["positions"][schema["op"]]
@@ -83,12 +98,19 @@ class Plug:
                 src.update(suh1=(d["suh1"], rp.F16), dn_suh=(d["dn_suh"], rp.F16))
                 dd = self.dev.tabs["dn"][cl]
                 src.update(dn_codes=(dd["codes"], rp.U8), dn_svh=(dd["svh"], rp.F16))
+            r, k = d["rows"], d["cols"]
+            ext = {"codes": (r, k), "suh": (k,), "suh1": (k,), "svh": (r,), "dn_suh": (r // 2,),
+                   "dn_codes": (k, r // 2), "dn_svh": (k,)}
             for p, name in enumerate(PLANES):
                 at = pos["plane"][cl][p]
                 if at >= 0 and name in src:
-                    ts[at] = _t2(*src[name])
+                    t, dt = src[name]
+                    if ptr:                                   # entries stored records (codes) / f16 vectors
+                        ts[at] = self._ptr_table(t, rp.DT_TRELLIS if "codes" in name else dt, ext[name])
+                    else:
+                        ts[at] = _t2(t, dt)
         params = self.params(si, **extra)
-        args = rp.Args(params.arr, params.n, ts, n, None, 0, None)
+        args = rp.Args(params.arr, params.n, ts, n, None, 0, inst)
         row = self.lib.rad_kernel_at(si).contents
         need = row.scratch(C.byref(args))     # a geometry the op refuses is refused here too (then so is the launch)
         scratch = self.dev.torch.empty(max(need, 256), dtype=self.dev.torch.uint8, device="cuda")
@@ -99,8 +121,8 @@ class Plug:
         return rc
 
 
-def _every_op(dev, base):
-    """Rows base+0..3 (two-class: 0..3, four-class: 4..7) against the C-ABI results."""
+def _every_op(dev, base, ptr=False):
+    """Rows base+0..3 (two-class: 0..3, four-class: 4..7) against the C-ABI results; ptr: pointer tables."""
     p = Plug(dev)
     torch, c = dev.torch, dev.case
     W = max(d["rows"] for d in dev.tabs["gu"]) // 2
@@ -109,7 +131,7 @@ def _every_op(dev, base):
     # prep_gu
     want = dev.prep()
     y = dev.out(2 * H, fill=-1)
-    assert p.run(base + 2, dev.x, y, rp.F16) == 0
+    assert p.run(base + 2, dev.x, y, rp.F16, ptr=ptr) == 0
     assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
     xr = torch.from_numpy(want.view(np.int16)).cuda()
     # gate_up, every (h_rot, a_rot)
@@ -117,7 +139,7 @@ def _every_op(dev, base):
         want = dev.gate_up(h_rot=h_rot)
         for a_rot in (0, 1):
             y = dev.out(W)
-            assert p.run(base + 0, xr if a_rot else dev.x, y, rp.F16, h_rot=h_rot, a_rot=a_rot) == 0
+            assert p.run(base + 0, xr if a_rot else dev.x, y, rp.F16, ptr=ptr, h_rot=h_rot, a_rot=a_rot) == 0
             assert np.array_equal(y.cpu().numpy().view(np.uint16), want), (h_rot, a_rot)
         if h_rot == 0:
             h0 = want
@@ -127,13 +149,14 @@ def _every_op(dev, base):
         want = dev.down(h, h_rot=h_rot)
         hd = torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).cuda()
         y = dev.out(N)
-        assert p.run(base + 1, hd, y, rp.BF16, h_rot=h_rot) == 0
+        assert p.run(base + 1, hd, y, rp.BF16, ptr=ptr, h_rot=h_rot) == 0
         assert np.array_equal(y.cpu().numpy().view(np.uint16), want), h_rot
     # gate_up_down
     want = dev.gate_up_down()
     y = dev.out(H)
-    assert p.run(base + 3, dev.x, y, rp.BF16) == 0
+    assert p.run(base + 3, dev.x, y, rp.BF16, ptr=ptr) == 0
     assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+    dev.check_guards("plugin rows")
 
 
 def test_plugin_rows_two_classes(torch_cuda):
@@ -168,3 +191,55 @@ def test_plugin_refusals_write_nothing(torch_cuda):
     assert p.run(0, dev.x, y, rp.F16, h_rot=3, a_rot=0) == rp.E_INVAL
     assert p.run(0, dev.x, y, rp.F16, h_rot=0, a_rot=0, dtype="exl3k9") == rp.E_DTYPE
     assert (y.cpu().numpy() == 0x1234).all() and (y2.cpu().numpy() == 0x1234).all()
+
+
+@pytest.mark.parametrize("name,base", [("two-class", 0), ("four-class", 4)])
+def test_plugin_rows_with_pointer_tables(torch_cuda, name, base):
+    """The engine's table form: every plane a device array of entry addresses (stride 0)."""
+    geoms = {"two-class": [(256, 256), (384, 128)], "four-class": [(256, 128), (256, 256), (128, 128), (256, 128)]}
+    case = Case(seed=35 + base, n_tok=8, top_k=6, n_expert=13, geoms=geoms[name], bits=4, cb="mul1", drop=0.1)
+    assert case.T >= 32                                # gate_up_down as its single kernel reads the tables too
+    print(f"plugin rows: {name}, pointer tables", flush=True)
+    _every_op(Dev(case), base, ptr=True)
+
+
+def _gd_inst(p, si):
+    row = p.lib.rad_kernel_at(si).contents
+    params = p.params(si)
+    inst = C.c_void_p()
+    assert row.init(params.arr, params.n, 0, 1, C.byref(inst)) == 0
+    assert inst.value, "the gate_up_down row's init made no instance"
+    return row, inst
+
+
+def test_gate_up_down_row_instance_counter_pool(torch_cuda):
+    """The row instance's counter blocks: the same bits as exl3c4_launch, one block per (stream, output), each left
+    zero; a launch whose block's flag says a wait gave up returns RAD_E_DEVICE, writes nothing, and the block serves
+    the next launch normally."""
+    case = Case(seed=39, n_tok=8, top_k=10, n_expert=40, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
+    assert case.T >= 32
+    dev = Dev(case)
+    p = Plug(dev)
+    want = dev.gate_up_down()
+    row, inst = _gd_inst(p, 3)
+    try:
+        H = dev.tabs["gu"][0]["cols"]
+        y1, y2 = dev.out(H), dev.out(H)
+        print("instance: two outputs, two launches each", flush=True)
+        for _ in range(2):
+            for y in (y1, y2):
+                assert p.run(3, dev.x, y, rp.BF16, inst=inst) == 0
+                assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+        assert p.lib.exl3c4_plugin_inst_blocks_used(inst) == 2
+        assert p.lib.exl3c4_plugin_inst_flag(inst, 0, -1) == 0 and p.lib.exl3c4_plugin_inst_flag(inst, 1, -1) == 0
+        print("instance: block 0 flagged as a wait that gave up", flush=True)
+        assert p.lib.exl3c4_plugin_inst_flag(inst, 0, 1) == 0       # force the failure path from the host
+        y1.fill_(0x1111)
+        assert p.run(3, dev.x, y1, rp.BF16, inst=inst) == -21       # RAD_E_DEVICE, nothing written
+        assert (y1.cpu().numpy() == 0x1111).all()
+        assert p.lib.exl3c4_plugin_inst_flag(inst, 0, -1) == 0
+        assert p.run(3, dev.x, y1, rp.BF16, inst=inst) == 0
+        assert np.array_equal(y1.cpu().numpy().view(np.uint16), want)
+        dev.check_guards("instance launches")
+    finally:
+        row.fini(inst)

@@ -46,6 +46,10 @@ def test_rows(lib):
         assert lib.rad_kernel_concurrent(i) == 1
         keys = {row.constraints[j].key for j in range(row.n_constraints)}
         assert b"dtype" in keys and b"K" in keys
+        # the gate_up_down rows keep instance state (a counter-block pool: init allocates, fini frees); no other row
+        gd = TABLES["schemas"][i]["op"].startswith("moe_exl3_gate_up_down")
+        assert bool(row.init) == gd and bool(row.fini) == gd
+        assert b"two launches" not in row.computes
 
 
 # geometries whose classes all differ, so that each plane table of each class has extents of its own
