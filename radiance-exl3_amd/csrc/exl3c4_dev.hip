@@ -50,8 +50,13 @@ constexpr float kHadScale = 0.08838834764831844055f;   // (float)(1/sqrt(128)), 
 
 // ------------------------------------------------------------------------------------------------ scalar helpers
 
+// Entry j of a per-expert table: base + j x stride, or with stride 0 the j-th pointer of a pointer table. The table
+// is read as constant memory (it does not change during a launch), so a uniform j is a scalar load, counted apart
+// from the vector loads: the vector loads in flight around it (codes, activations) are not waited for at the join.
+typedef const void* cvptr;
 __device__ __forceinline__ const void* tab_entry(const void* base, int32_t stride, int64_t j) {
-    return stride ? (const void*)((const char*)base + j * (int64_t)stride) : ((const void* const*)base)[j];
+    return stride ? (const void*)((const char*)base + j * (int64_t)stride)
+                  : ((const __attribute__((address_space(4))) cvptr*)base)[j];
 }
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -303,11 +308,13 @@ __device__ __forceinline__ int perm_slot(int k) {
 }
 
 // The owner of sorted row i and its run (include/exl3_abi.h:136-141), found by a whole workgroup in ONE round of
-// independent loads: its threads read off[1 .. n_expert], count by wave ballots the e with off[e] <= i (for sorted
+// independent loads: its threads read off[0 .. n_expert] (four entries a thread in flight together, the addresses
+// clamped so that no load sits behind a branch), count by wave ballots the e >= 1 with off[e] <= i (for sorted
 // offsets, the owner's number) and keep the offsets in LDS, so the run's bounds off[e], off[e + 1] come from there
 // after the barrier instead of a second round of loads (up to OWNER_LDS experts; beyond, from memory). The row has an
 // owner when e < n_expert and off[e] <= i < off[e + 1]; else -1. lo / hi: the run clamped to [0, T)
-// (kernels/exl3r4d/launch.c:14-15). Holds a barrier: every thread of the workgroup calls it.
+// (kernels/exl3r4d/launch.c:14-15). The result is uniform (in scalar registers): the class tables it selects are read
+// with scalar loads. Holds a barrier: every thread of the workgroup calls it.
 struct Owner { int e, lo, hi; };
 constexpr int OWNER_LDS = 1024;
 __device__ Owner owner_wg(const Exl3c4Launch& a, int i) {
@@ -315,16 +322,22 @@ __device__ Owner owner_wg(const Exl3c4Launch& a, int i) {
     __shared__ int off_s[OWNER_LDS + 1];
     const int n = a.n_expert, tid = (int)threadIdx.x;
     int cnt = 0;
-    for (int e0 = 0; e0 <= n; e0 += 256) {                        // uniform trip count: ballots see every lane
-        const int e = e0 + tid;
-        const int o = e <= n ? a.off[e] : 0x7FFFFFFF;
-        if (e <= OWNER_LDS && e <= n) off_s[e] = o;
-        cnt += __popcll(__ballot(e >= 1 && o <= i));
+    for (int e0 = 0; e0 <= n; e0 += 4 * 256) {                    // uniform trip count: ballots see every lane
+        int o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = a.off[min(e0 + 256 * j + tid, n)];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = e0 + 256 * j + tid;
+            if (e <= OWNER_LDS && e <= n) off_s[e] = o[j];
+            cnt += __popcll(__ballot(e >= 1 && e <= n && o[j] <= i));
+        }
     }
     if ((tid & 63) == 0) cnt_s[tid >> 6] = cnt;
     __syncthreads();
-    const int e = min(cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3], n - 1);
-    const int o0 = e + 1 <= OWNER_LDS ? off_s[e] : a.off[e], o1 = e + 1 <= OWNER_LDS ? off_s[e + 1] : a.off[e + 1];
+    const int e = __builtin_amdgcn_readfirstlane(min(cnt_s[0] + cnt_s[1] + cnt_s[2] + cnt_s[3], n - 1));
+    const int o0 = __builtin_amdgcn_readfirstlane(e + 1 <= OWNER_LDS ? off_s[e] : a.off[e]);
+    const int o1 = __builtin_amdgcn_readfirstlane(e + 1 <= OWNER_LDS ? off_s[e + 1] : a.off[e + 1]);
     Owner w;
     w.e = (o0 <= i && i < o1) ? e : -1;
     w.lo = max(o0, 0);
@@ -535,15 +548,80 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r
                                            float4_t& acc0, float4_t& acc1) {
     const Mul1Consts k = mul1_consts();
     constexpr int PF = EXL3C4_GEMV_PF;
-    // ksn is even (two steps a 128-block) and PF two, so both steps of a pair exist; the refill is unconditional (past
-    // the stream a harmless reload of the last step), so the waits for the codes are counted, not drained
-    static_assert(PF == 2, "gemv_strip runs its steps in pairs");
+    // ksn is even (two steps a 128-block), so with PF two both steps of a pair exist; a deeper ring ends the stream
+    // with a partial round. The refill is unconditional (past the stream a harmless reload of the last step), so the
+    // waits for the codes are counted, not drained.
+    static_assert(PF >= 2 && PF <= 4, "gemv_strip keeps two to four steps in flight");
     for (int s = 0; s < ksn; s += PF) {
 #pragma unroll
         for (int q = 0; q < PF; ++q) {
+            if (PF > 2 && s + q >= ksn) break;
             mma_step<BITS, CB>(r.d[q], arow + (s + q) * EXL3C4_KSTEP, k, acc0, acc1);
             const int nx = s + q + PF < ksn ? s + q + PF : ksn - 1;
             load_words<BITS>(rec + nx * 64 * BITS, r.d[q]);
+        }
+    }
+}
+
+// gate_up's staging of a split's input rows in LDS (the split's 128-blocks [b0, b1), wave w taking hb = b0 + w + 4 j):
+// as given (AROT: x holds the rotated rows, the gate half then the up half) or f16(had128(f16(x * s))) of the row's
+// token (s = suh or suh1, zero for a negative sorted_tok). Up to GU_WB blocks of the wave have their scale and input
+// loads issued together, a row at a time, none of them behind a branch (addresses clamped: a block past the split
+// loads the split's last one, unused), so a row costs one memory round trip; wider splits take the rest one block at
+// a time. The first row's input, the codes' first steps and the scales go out together (one round trip); the codes
+// are not waited for before the loop.
+template <int BITS, bool AROT>
+__device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows, int KC, bool up, int b0, int b1,
+                                         int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
+                                         uint16_t* A, int kp) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int GU_WB = 4;
+    const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
+    const bool bf = a.x_dtype == EXL3C4_BF16;
+    int hbj[GU_WB];
+    uint16_t s0[GU_WB], s1[GU_WB];
+#pragma unroll
+    for (int j = 0; j < GU_WB; ++j) hbj[j] = min(b0 + wave + 4 * j, b1 - 1);
+    for (int q = 0; q < nrows; ++q) {
+        const int tok = AROT ? 0 : __builtin_amdgcn_readlane(tok_l, q);
+        int64_t src = AROT ? (int64_t)i + q : (tok >= 0 ? tok / a.top_k : 0);
+        src = src < a.x_rows ? src : a.x_rows - 1;
+        const uint16_t* xr = (const uint16_t*)a.x + src * a.x_pitch + (AROT && up ? KC : 0);
+        uint16_t x0[GU_WB], x1[GU_WB];
+#pragma unroll
+        for (int j = 0; j < GU_WB; ++j) {
+            x0[j] = ldg16(xr, hbj[j] * 128 + lane);
+            x1[j] = ldg16(xr, hbj[j] * 128 + 64 + lane);
+        }
+        if (q == 0) {                        // then the codes' first steps and the scales: one round trip for all
+            prime<BITS>(rec, ksn, ring);
+#pragma unroll
+            for (int j = 0; j < GU_WB; ++j) {
+                s0[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + lane);
+                s1[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + 64 + lane);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < GU_WB; ++j) {
+            if (j >= nbw) break;
+            uint16_t v0 = x0[j], v1 = x1[j];
+            if (!AROT) {
+                v0 = v1 = 0;
+                if (tok >= 0)
+                    rotate_block(bf ? bf2f(x0[j]) : h2f(x0[j]), bf ? bf2f(x1[j]) : h2f(x1[j]), s0[j], s1[j], lane, v0,
+                                 v1);
+            }
+            lds_put(A, q, kp, (hbj[j] - b0) * 128, lane, v0, v1);
+        }
+        for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
+            const uint16_t y0 = ldg16(xr, hb * 128 + lane), y1 = ldg16(xr, hb * 128 + 64 + lane);
+            const uint16_t t0 = AROT ? 0 : ldg16(sv, hb * 128 + lane), t1 = AROT ? 0 : ldg16(sv, hb * 128 + 64 + lane);
+            uint16_t v0 = y0, v1 = y1;
+            if (!AROT) {
+                v0 = v1 = 0;
+                if (tok >= 0) rotate_block(bf ? bf2f(y0) : h2f(y0), bf ? bf2f(y1) : h2f(y1), t0, t1, lane, v0, v1);
+            }
+            lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
         }
     }
 }
@@ -562,29 +640,20 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int S = a.ksplit;
     const int grp = u >> a.ksplit_log2, split = u & (S - 1);
-    // The start-up (owner, staging) runs at a raised wave priority, the GEMV loop at 0: a unit still starting when
-    // the others' loops run is not starved of issue slots, so gate_up's units finish together.
-    __builtin_amdgcn_s_setprio(2);
     // the chunk's sorted_tok (lane q: row i + q), read beside the owner search (taken by readlane below)
-    const int tok_l = a.a_rot ? 0 : a.sorted[min(i + (lane & 15), a.T - 1)];
+    const int tok_l = a.sorted[min(i + (lane & 15), a.T - 1)];
     const Owner w = owner_wg(a, i);
     const int nrows = chunk_rows(a, w, i);
     if (!FUSED && u == 0 && threadIdx.x == 0) {
         a.row_info[2 * i] = w.e;
         a.row_info[2 * i + 1] = nrows;
     }
-    if (nrows == 0) {
-        __builtin_amdgcn_s_setprio(0);
-        return GuRows{ 0, w.e };
-    }
+    if (nrows == 0) return GuRows{ 0, w.e };
     const int c = class_of(a, w.e);
     const int64_t jx = entry_of(a, w.e);
     const Exl3c4DevClass& K = a.cls[c];
     const int N = K.rows, KC = K.cols;
-    if (grp * 128 >= N) {
-        __builtin_amdgcn_s_setprio(0);
-        return GuRows{ nrows, w.e };
-    }
+    if (grp * 128 >= N) return GuRows{ nrows, w.e };
     const int strip = grp * 4 + wave;
     const bool up = grp * 128 >= N / 2;
     const int nb = KC / 128, per = (nb + S - 1) / S;
@@ -595,67 +664,13 @@ __device__ __forceinline__ GuRows gu_unit(const Exl3c4Launch& a, int i, int u, i
     CodeRing<BITS> ring;
 
     uint16_t* A = (uint16_t*)lds;                                 // [chunk_rows][kp]
-    const void* sv = up ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx);
-    // The wave's 128-blocks hb = b0 + wave + 4 j of the split: up to GU_WB of them have their scale and input loads
-    // issued together, a row at a time, before any rotation (one memory round trip a row, not one a block); the
-    // addresses of blocks past the split are clamped (loaded, unused). Wider splits take the rest one at a time.
-    constexpr int GU_WB = 4;
-    const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
     if (ksn > 0) {
-        int hbj[GU_WB];
-        uint16_t s0[GU_WB], s1[GU_WB];
-#pragma unroll
-        for (int j = 0; j < GU_WB; ++j) {
-            hbj[j] = min(b0 + wave + 4 * j, b1 - 1);
-            s0[j] = a.a_rot ? 0 : ldg16(sv, hbj[j] * 128 + lane);
-            s1[j] = a.a_rot ? 0 : ldg16(sv, hbj[j] * 128 + 64 + lane);
-        }
-        for (int q = 0; q < nrows; ++q) {
-            const int64_t r = i + q;
-            const int tok = a.a_rot ? 0 : __builtin_amdgcn_readlane(tok_l, q);
-            int64_t src = a.a_rot ? r : (tok >= 0 ? tok / a.top_k : 0);
-            src = src < a.x_rows ? src : a.x_rows - 1;
-            const uint16_t* xr = (const uint16_t*)a.x + src * a.x_pitch + (a.a_rot && up ? KC : 0);
-            uint16_t x0[GU_WB], x1[GU_WB];
-#pragma unroll
-            for (int j = 0; j < GU_WB; ++j) {
-                x0[j] = ldg16(xr, hbj[j] * 128 + lane);
-                x1[j] = ldg16(xr, hbj[j] * 128 + 64 + lane);
-            }
-            // the codes' first steps go out behind the first row's input (loads complete in order: the staging
-            // waits for its own loads only) and fly during the rotation
-            if (q == 0) prime<BITS>(rec, ksn, ring);
-#pragma unroll
-            for (int j = 0; j < GU_WB; ++j) {
-                if (j >= nbw) break;
-                uint16_t v0 = 0, v1 = 0;
-                if (a.a_rot) {
-                    v0 = x0[j];
-                    v1 = x1[j];
-                } else if (tok >= 0) {
-                    const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0[j]) : h2f(x0[j]);
-                    const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1[j]) : h2f(x1[j]);
-                    rotate_block(f0, f1, s0[j], s1[j], lane, v0, v1);
-                }
-                lds_put(A, q, kp, (hbj[j] - b0) * 128, lane, v0, v1);
-            }
-            for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
-                uint16_t v0 = 0, v1 = 0;
-                const uint16_t y0 = ldg16(xr, hb * 128 + lane), y1 = ldg16(xr, hb * 128 + 64 + lane);
-                if (a.a_rot) {
-                    v0 = y0;
-                    v1 = y1;
-                } else if (tok >= 0) {
-                    const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(y0) : h2f(y0);
-                    const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(y1) : h2f(y1);
-                    rotate_block(f0, f1, ldg16(sv, hb * 128 + lane), ldg16(sv, hb * 128 + 64 + lane), lane, v0, v1);
-                }
-                lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
-            }
-        }
+        if (a.a_rot) gu_stage<BITS, true>(a, i, nrows, KC, up, b0, b1, tok_l, nullptr, rec, ksn, ring, A, kp);
+        else gu_stage<BITS, false>(a, i, nrows, KC, up, b0, b1, tok_l,
+                                   up ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx), rec, ksn,
+                                   ring, A, kp);
     }
     __syncthreads();
-    __builtin_amdgcn_s_setprio(0);
 
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
     gemv_strip<BITS, CB>(rec, ksn, ring, A + a_row(a, lane) * kp + 16 * (lane >> 4), acc0, acc1);
@@ -773,10 +788,15 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
             if (t >= 0 && t < a.g_ntok) {
                 const int old = __hip_atomic_fetch_add(a.g_ctr + (int64_t)t * EXL3C4_SYNC_STRIDE + b, 1,
                                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                int need = 0;                                     // read while the count is in flight
-                for (int s = 0; s < a.top_k; ++s) {              // a slot has a row when 0 <= row < T, as the
-                    const int r = a.g_row_of[(int64_t)t * a.top_k + s];   // sum and gather_empty read it
-                    need += (r >= 0 && r < a.T) ? 1 : 0;
+                // the token's slots with a row (0 <= row < T, as the sum and gather_empty read it), read while the
+                // count is in flight: 16 slots' loads at once (clamped addresses, none behind a branch)
+                int need = 0;
+                for (int s0 = 0; s0 < a.top_k; s0 += 16) {
+                    int r[16];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) r[u] = a.g_row_of[(int64_t)t * a.top_k + min(s0 + u, a.top_k - 1)];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) need += (s0 + u < a.top_k && r[u] >= 0 && r[u] < a.T) ? 1 : 0;
                 }
                 last = old == need - 1;
             }
@@ -792,14 +812,17 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
         const int c = b * 128 + lane;
         float acc0 = 0.f, acc1 = 0.f;
         for (int s0 = 0; s0 < a.top_k; s0 += 16) {                // 16 slots' rows and weights, then their values
+            // lane u reads slot s0 + u (one round trip for all 16), each then taken uniform by readlane
+            const int sl_l = min(s0 + (lane & 15), a.top_k - 1);
+            const int r_l = a.g_row_of[t * a.top_k + sl_l];
+            const float w_l = a.g_w[t * a.top_k + sl_l];
             int r[16];
             float w[16];
             uint16_t q0[16], q1[16];
 #pragma unroll
             for (int u = 0; u < 16; ++u) {
-                const int sl = min(s0 + u, a.top_k - 1);
-                r[u] = a.g_row_of[t * a.top_k + sl];
-                w[u] = a.g_w[t * a.top_k + sl];
+                r[u] = __builtin_amdgcn_readlane(r_l, u);
+                w[u] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w_l), u));
                 if (s0 + u >= a.top_k || r[u] >= a.T) r[u] = -1;
             }
 #pragma unroll
@@ -830,9 +853,9 @@ __device__ __forceinline__ void gather_empty(const Exl3c4Launch& a, int z) {
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)z * 4 + (threadIdx.x >> 6);        // k_gd: 4 waves a workgroup
     if (t >= a.g_ntok) return;
-    for (int s = 0; s < a.top_k; ++s) {
-        const int r = a.g_row_of[t * a.top_k + s];
-        if (r >= 0 && r < a.T) return;
+    for (int s0 = 0; s0 < a.top_k; s0 += 64) {                    // lane u reads slot s0 + u
+        const int r = a.g_row_of[t * a.top_k + min(s0 + lane, a.top_k - 1)];
+        if (__ballot(s0 + lane < a.top_k && r >= 0 && r < a.T)) return;
     }
     for (int c = lane; c < a.y_cols; c += 64) a.g_out[t * a.g_out_pitch + c] = 0;
 }
@@ -848,11 +871,10 @@ __device__ __forceinline__ DnW dn_weight(bool gd, const Exl3c4DevClass& K) {
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __builtin_amdgcn_s_setprio(2);                                // the start-up at a raised priority (gu_unit)
     int e, nrows;
-    if (!FUSED && a.row_info) {
-        e = a.row_info[2 * i];
-        nrows = a.row_info[2 * i + 1];
+    if (!FUSED && a.row_info) {                                   // uniform: the class tables by scalar loads
+        e = __builtin_amdgcn_readfirstlane(a.row_info[2 * i]);
+        nrows = __builtin_amdgcn_readfirstlane(a.row_info[2 * i + 1]);
     } else {
         const Owner w = owner_wg(a, i);
         e = w.e;
@@ -905,17 +927,15 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
 
     // stage the chunk's rows
     const int nhb = KC / 128;
-    if (FUSED && nhb <= 4) {                                      // each wave one block of h: every row's loads first
-        constexpr int R = EXL3C4_CHUNK_ROWS;
-        const int hb = wave;
+    if (FUSED && nhb <= 4) {                                      // each wave one block of h: every row's loads first,
+        constexpr int R = EXL3C4_CHUNK_ROWS;                      // none behind a branch (rows past the chunk's last
+        const int hb = wave;                                      // and blocks past h's last load those, unused)
         uint16_t h0[R], h1[R];
 #pragma unroll
         for (int q = 0; q < R; ++q) {
             const uint16_t* hs = a.hbuf + (int64_t)(i + min(q, nrows - 1)) * a.hbuf_pitch + min(hb, nhb - 1) * 128;
-            if (q < a.chunk_rows) {
-                h0[q] = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                h1[q] = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            h0[q] = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            h1[q] = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 #pragma unroll
         for (int q = 0; q < R; ++q)
@@ -946,7 +966,6 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     }
     __syncthreads();
 
-    __builtin_amdgcn_s_setprio(0);
     float4_t acc0 = { 0.f, 0.f, 0.f, 0.f }, acc1 = { 0.f, 0.f, 0.f, 0.f };
     gemv_strip<BITS, CB>(rec, ksteps, ring, A + a_row(a, lane) * kp + 16 * (lane >> 4), acc0, acc1);
 
@@ -991,7 +1010,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
 // from the rows' partial sums, once, by the row's last gate_up unit: into hbuf, then one more count on row i's counter.
 __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows& g) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __builtin_amdgcn_s_setprio(2);                                // every down unit of the row waits for this
     const int c = class_of(a, g.e);
     const int64_t jx = entry_of(a, g.e);
     const Exl3c4DevClass& G = a.cls[c];
@@ -999,8 +1017,9 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
     for (int t = wave; t < g.nrows * nhb; t += 4) {
         const int q = t / nhb, hb = t - q * nhb;
         const int64_t r = i + q;
-        uint16_t v0 = 0, v1 = 0;
-        if (a.sorted[r] >= 0) gate_up_block<true>(a, G, r, hb, jx, 1, lane, v0, v1);
+        uint16_t v0, v1;                                          // the row's loads and sorted_tok's together
+        gate_up_block<true>(a, G, r, hb, jx, 1, lane, v0, v1);
+        if (a.sorted[r] < 0) v0 = v1 = 0;
         uint16_t* h = a.hbuf + r * a.hbuf_pitch + hb * 128;
         __hip_atomic_store(h + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(h + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1008,7 +1027,6 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_fetch_add(row_counter(a, i), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_setprio(0);
 }
 
 // gate_up_down in one launch (decode path). Workgroups g = 8 k + x (x < 8) take the sorted rows i = x (mod 8): first

@@ -54,20 +54,21 @@ static int64_t chunk_bound(int64_t T, int64_t n_expert, int ch) {
 }
 
 /* gate_up's split-K on the decode path, from T, M and the geometry (never the routing): the most splits -- a power of
- * two, at most 16 and at most one a 128-block of k -- that still leave every gate_up unit of the launch resident at
- * once (GU_SLOTS workgroups: 256 CUs x 7), so that gate_up_down's single kernel runs all of gate_up as one phase at
- * full occupancy and every row's down units follow it, with no late round of gate_up units whose down units would
- * run after it alone; then more splits while a split's staged rows would take more LDS than GU_LDS_BUDGET (which
+ * two, at most 16 and at most one a 128-block of k -- that keep the launch's gate_up units (chunks x n_grp x S) at
+ * most GU_UNITS. A split shortens a unit's chain of code loads (and so the wait of the row's down units for its last
+ * gate_up unit) and adds a unit's fixed start-up; on configs[2] (80 chunks x 8 groups) S = 4, 2560 units against
+ * about 1790 resident workgroups, measured 1.7 us a layer step faster than S = 2 (every unit resident at once) and
+ * 5 us faster than S = 8. Then more splits while a split's staged rows would take more LDS than GU_LDS_BUDGET (which
  * keeps 7 workgroups a CU). */
-#ifndef GU_SLOTS
-#define GU_SLOTS 1792
+#ifndef GU_UNITS
+#define GU_UNITS 4096
 #endif
 #ifndef GU_LDS_BUDGET
 #define GU_LDS_BUDGET (20 * 1024)
 #endif
 static int ksplit_for(int64_t chunks, int64_t n_grp, int64_t nb_min, int64_t nb_max, int ch) {
     int s = 1;
-    while (s < 16 && 2 * s <= nb_min && chunks * n_grp * 2 * s <= GU_SLOTS) s *= 2;
+    while (s < 16 && 2 * s <= nb_min && chunks * n_grp * 2 * s <= GU_UNITS) s *= 2;
     while (s < 16 && 2 * s <= nb_max && (int64_t)ch * (((nb_max + s - 1) / s) * 128 + 8) * 2 > GU_LDS_BUDGET) s *= 2;
     return s;
 }
