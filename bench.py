@@ -2,20 +2,23 @@
 """bench.py -- throughput of the EXL3 routed-expert decode layer on one MI355X; with
 --config 2, 4 or 5 the single expert, the prefill layer or the 48-layer decode stack instead.
 
-One STEP is one routed-MoE layer in decode: 8 tokens (2 sequences x 4 speculative positions) through 512 experts at
-4 bpw (gate/up 2048 -> 2 x 512, down 512 -> 2048, codebook mul1), router softmax -> top-10 -> renormalised, as ONE
-moe_exl3_gate_up_down launch of libexl3c4.so (prep, gate_up with the h_rot epilogue, down). The router, the scatter and
-the gather are the engine's ops in the reference (include/exl3_abi.h:90-118) and run outside the timed region.
+One STEP is one routed-MoE layer in decode, the whole layer on the device: 8 tokens (2 sequences x 4 speculative
+positions) through 512 experts at 4 bpw (gate/up 2048 -> 2 x 512, down 512 -> 2048, codebook mul1): the router
+(softmax over N(0,1) logits -> top-10 -> renormalised) with the stable scatter by expert, then ONE
+moe_exl3_gate_up_down launch of libexl3c4.so whose single kernel also does moe_gather (the weighted sum in f32, cast to
+f16). The same step with the gather as its own dispatch, and the op alone, are timed beside it.
 
 Measurement hygiene: all experts of `--layers` independent layers are resident in HBM (about 0.8 GB a layer) and every
 step uses the next layer and the next of `--draws` routing draws, so the ~120 MB a step reads was not read in the
 previous several hundred MB (MI355X's 256 MB Infinity Cache). The timed steps are captured once into a HIP graph and
 replayed, so host launch cost does not pace the GPU. Inputs are resident before the timed region starts.
 
-Prints ONE JSON line. `value` is tokens/s of the layer; `roofline` is the dominant kernel's (gate_up's trellis-decode
-GEMV) achieved packed-weight bandwidth against the 8 TB/s HBM peak, its duration timed live by events the dispatch
-itself stamps; `cpu_baseline` times the CPU oracle (this repository's C restatement of the reference's exl3ref, one
-thread) on a bounded sample of the same workload.
+Prints ONE JSON line. `value` is tokens/s of the layer; `roofline` is the dominant kernel's (gate_up_down's single
+kernel) achieved packed-weight bandwidth against the 8 TB/s HBM peak, its duration timed live by events the dispatch
+itself stamps; `roofline_valu` the same kernel against the VALU issue rate its trellis decode is bound by; `prefill`
+the prefill layer (configs[3]: 2048 tokens, Zipf routing) measured in the same run; `cpu_baseline` times the CPU
+oracle (this repository's C restatement of the reference's exl3ref) on the same workload, on one thread and on the
+box's cores.
 """
 from __future__ import annotations
 
@@ -80,9 +83,21 @@ def build_draws(torch, n_draws, seed):
     return draws
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(draw, max_experts, seed):
-    """The oracle's gate_up_down (scalar, one thread) on the live experts of one routing draw -- or the first
-    `max_experts` of them, the time scaled to all -- with freshly drawn canonical planes of the same geometry."""
+    """The oracle's gate_up_down on the live experts of one routing draw -- or the first `max_experts` of them, the
+    time scaled to all -- with freshly drawn canonical planes of the same geometry: once on one thread, once on the
+    box's cores (the oracle spreads live experts over OpenMP threads; its outputs do not depend on the count)."""
     import exl3c4_synth as syn
     import oracle
     rng = np.random.default_rng(seed)
@@ -102,14 +117,20 @@ def cpu_baseline(draw, max_experts, seed):
           "suh": gu["dn_suh"], "svh": syn.sign_scales(rng, H, 1 / np.sqrt(W), n)}
     x = draw["x_np"].view(np.uint16)
     oracle.lib()
-    t0 = time.perf_counter()
-    oracle.run_gate_up_down([gu], [dn], BITS, CB, x, sub_st, sub_off, TOP_K)
-    dt = time.perf_counter() - t0
-    t_layer = dt * len(live) / n
-    return {"value": round(M / t_layer, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+    times = {}
+    for threads in (1, oracle.default_threads()):
+        oracle.set_threads(threads)
+        t0 = time.perf_counter()
+        oracle.run_gate_up_down([gu], [dn], BITS, CB, x, sub_st, sub_off, TOP_K)
+        times[threads] = time.perf_counter() - t0
+    cores = max(times)
+    scale = len(live) / n
+    return {"value": round(M / (times[cores] * scale), 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "value_1thread": round(M / (times[1] * scale), 3), "nproc": os.cpu_count(), "cpu_model": cpu_model(),
             "sample": (f"{n} of the {len(live)} live experts of one decode layer step (8 tokens, top-10, K=4 mul1), "
-                       f"oracle/exl3_oracle.c gate_up_down on 1 thread: {dt:.2f} s, scaled x{len(live) / n:.2f} "
-                       f"to the whole layer")}
+                       f"oracle/exl3_oracle.c gate_up_down: {times[1]:.2f} s on 1 thread, {times[cores]:.2f} s on "
+                       f"{cores} (OpenMP over experts)" + (f", scaled x{scale:.2f} to the whole layer" if n < len(live)
+                                                         else ""))}
 
 
 def read_traffic(name):
@@ -249,9 +270,29 @@ def run_decode_layer(args, torch, exl3c4):
                      "kernel": "k_gd<4,mul1> (gate_up_down, one kernel)" if one else "k_gu<4,mul1> (gate_up GEMM)",
                      "avg_us": round(float(np.mean(durs)) * 1e3, 3),
                      "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
+        "roofline_valu": valu_roofline(float(np.mean(gemv_bytes)) * 8 / BITS, float(np.mean(durs)) * 1e-3),
         "cpu_baseline": cpu,
     })
     return out
+
+
+# The decode loop's VALU work, read from the gfx950 assembly of k_gd<4,mul1> (the same loop body in k_gu / k_dn): an
+# iteration of two steps -- each step a wave's 32-column strip over 64 k, 2048 weights -- issues 253 VALU instructions
+# (64 v_pk_mul_lo_u16, 64 v_mad_u32_u16, 32 v_sad_u8, 32 v_sad_hi_u8, 32 v_pk_fma_f16, 18 v_alignbit_b32, 6 v_perm_b32,
+# 5 others) and 8 MFMAs.
+VALU_PER_STEP, WEIGHTS_PER_STEP = 126.5, 2048
+# A SIMD issues one wave64 VALU instruction each 4 cycles (measured 1.8-1.95 ns each for the decode's instructions);
+# 1024 SIMDs at MI355X's 2.4 GHz peak engine clock.
+VALU_PEAK_GINSTR = 1024 * 2.4 / 4
+
+
+def valu_roofline(weights, seconds):
+    """The decode kernel against the VALU issue roofline: its loop's wave instructions over the kernel's duration."""
+    instr = weights / WEIGHTS_PER_STEP * VALU_PER_STEP
+    achieved = instr / seconds / 1e9
+    return {"bound": "valu", "achieved": round(achieved, 1), "peak": VALU_PEAK_GINSTR, "unit": "G wave-instr/s",
+            "frac": round(achieved / VALU_PEAK_GINSTR, 4), "instr_per_launch": round(instr),
+            "floor_us": round(instr / VALU_PEAK_GINSTR / 1e3, 2)}
 
 
 # ------------------------------------------------------------------------------------------ configs[1]: one expert
@@ -408,12 +449,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--layers", type=int, default=8)
     ap.add_argument("--draws", type=int, default=8)
-    ap.add_argument("--cpu-experts", type=int, default=24, help="live experts in the CPU-baseline sample (0: skip)")
+    ap.add_argument("--cpu-experts", type=int, default=E,
+                    help="live experts in the CPU-baseline sample (default: all of the layer's; 0: skip)")
     ap.add_argument("--seed", type=int, default=20261013)
     ap.add_argument("--config", type=int, default=3, choices=(2, 3, 4, 5),
                     help="BASELINE.json configs[n-1]: 2 one expert, 3 decode layer (default), 4 prefill layer, "
                          "5 48-layer decode stack")
     ap.add_argument("--stack-layers", type=int, default=48)
+    ap.add_argument("--no-prefill", dest="prefill", action="store_false",
+                    help="with the default decode layer: skip the prefill layer's figures")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 20 plain device-to-device copies of BYTES (the HBM-counter calibration) and exit")
     args = ap.parse_args()
@@ -435,7 +479,15 @@ def main():
     exl3c4.lib()
     torch.cuda.set_device(0)
     run = {2: run_single_expert, 3: run_decode_layer, 4: run_prefill_layer, 5: run_stack}[args.config]
-    print(json.dumps(run(args, torch, exl3c4)), flush=True)
+    out = run(args, torch, exl3c4)
+    if args.config == 3 and args.prefill:
+        # the prefill layer measured in the same run, its figures beside the decode line's
+        pf = run_prefill_layer(args, torch, exl3c4)
+        out["prefill"] = {"workload": pf["config"]["workload"], "rows": pf["config"]["rows"],
+                          "max_rows_per_expert": pf["config"]["max_rows_per_expert"],
+                          "us_per_layer": round(pf["ms_per_step"] * 1e3, 1), "tokens_per_s": pf["value"],
+                          "TFLOPs": pf["TFLOPs"], "mfma_frac": pf["mfma_frac"], "roofline": pf["roofline"]}
+    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

@@ -773,7 +773,7 @@ __device__ __forceinline__ void put_y(const Exl3c4Launch& a, uint16_t* out, int 
 // from row_of) gathers that token's block -- k_gather's sum: the slots in ascending order, one f32 product and one add
 // each, f16 -- over the rows' y read coherently, then sets the counter back to zero. No unit waits here. A chunk holds
 // a token at most once (its slots name distinct experts), at most 16 rows at decode.
-__device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
+__device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b, int tok_l) {
     __shared__ int tok_s[64];
     __shared__ int ntok_s;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");              // this thread's y stores are done
@@ -782,8 +782,8 @@ __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b) {
     if (wave == 0) {
         bool last = false;
         int t = -1;
-        if (lane < nrows) {
-            const int p = a.sorted[i + lane];
+        if (lane < nrows) {                                       // tok_l: sorted_tok of row i + lane
+            const int p = tok_l;
             t = p >= 0 ? p / a.top_k : -1;
             if (t >= 0 && t < a.g_ntok) {
                 const int old = __hip_atomic_fetch_add(a.g_ctr + (int64_t)t * EXL3C4_SYNC_STRIDE + b, 1,
@@ -871,6 +871,8 @@ __device__ __forceinline__ DnW dn_weight(bool gd, const Exl3c4DevClass& K) {
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the chunk's sorted_tok (lane q: row i + q), read beside the owner search: the epilogue and the gather take it
+    const int tok_l = a.sorted[min(i + (lane & 15), a.T - 1)];
     int e, nrows;
     if (!FUSED && a.row_info) {                                   // uniform: the class tables by scalar loads
         e = __builtin_amdgcn_readfirstlane(a.row_info[2 * i]);
@@ -896,7 +898,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     if (b * 128 >= N) {                                           // a narrower class's tail
         for (int q = wave; q < nrows; q += 4)
             put_y(a, (uint16_t*)a.y + (int64_t)(i + q) * a.y_pitch + b * 128, lane, 0, 0);
-        if (FUSED && a.g_out) gather_count(a, i, nrows, b);
+        if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
         return;
     }
     const int kp = a.lds_pitch;               // halves a staged row: k plus 8, so the 16 rows fall in different banks
@@ -990,14 +992,14 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         dacc[lane] = y0;
         dacc[lane + 64] = y1;
         uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
-        if (a.sorted[r] < 0) {
+        if (__builtin_amdgcn_readlane(tok_l, q) < 0) {
             put_y(a, out, lane, 0, 0);
             continue;
         }
         had128_wave(y0, y1, lane);
         put_y(a, out, lane, f2bf(y0 * h2f(sv0)), f2bf(y1 * h2f(sv1)));
     }
-    if (FUSED && a.g_out) gather_count(a, i, nrows, b);
+    if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
 }
 
 template <int BITS, int CB>
