@@ -51,6 +51,11 @@ enum {
     EXL3C4_E_UNSUPPORTED = -18,
     EXL3C4_E_SCRATCH = -20,
     EXL3C4_E_DEVICE = -21,
+    /* the import's (quantizers/exl3/exl3_quant.cpp:12-20 names them; radiance's values are not in the reference, these
+     * are this library's; FORMAT is include/rad_shim.h's) */
+    EXL3C4_E_FORMAT = -5,
+    EXL3C4_E_NOTFOUND = -30,
+    EXL3C4_E_IO = -31,
 };
 
 /* The ops, numbered as include/exl3_abi.h:292 numbers them. */
@@ -244,6 +249,42 @@ int exl3c4_relayout(const uint8_t* codes, int64_t row_bytes, int64_t rows, int64
 /* Stored record -> canonical plane (kernels/exl3r4d/layout.c:332-360): the bits of each row's elements are written,
  * the rest of the plane is left as it was. */
 int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes, int64_t row_bytes);
+/* exllamav3's tile record of a [rows, cols] weight (int16 [cols / 16][rows / 16][16 K], a checkpoint's .trellis) ->
+ * canonical plane (common/exl3_layout.c:38-56, exl3_record_to_codes). rows, cols in 16s, bits 1..8; row_bytes 0 =
+ * dense. */
+int exl3c4_record_to_codes(const uint16_t* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes,
+                           int64_t row_bytes);
+
+/* ------------------------------------------------------------------ the import (host, load time)
+ * Routed experts of an EXL3 checkpoint directory (exllamav3's safetensors layout: config.json with
+ * quantization_config.quant_method "exl3", model.safetensors or shards named by model.safetensors.index.json) into
+ * canonical planes: what the reference's `exl3` quantiser does (quantizers/exl3/exl3_quant.cpp:192-256; its reader
+ * quantizers/exl3/exl3_src.cpp). A checkpoint is opened once and may be shared by threads.
+ *   exl3c4_ckpt_open          EXL3C4_E_FORMAT: not an EXL3 checkpoint this reader understands (no config.json, another
+ *                             quant_method, no layer count, a malformed header or index); EXL3C4_E_IO
+ *   exl3c4_ckpt_layers        text_config.num_hidden_layers (or num_hidden_layers): layer index of the MTP head
+ *   exl3c4_import_parse_name  blk.L.ffn_gate_up_exps.E.weight (stacked 1) | blk.L.ffn_down_exps.E.weight (stacked 0);
+ *                             anything else EXL3C4_E_UNSUPPORTED (exl3_quant.cpp:97-114)
+ *   exl3c4_import_weight      the named weight [rows, cols] (stacked: gate rows then up rows) into codes (uK, rows
+ *                             row_bytes apart), suh [cols], suh1 [cols] (stacked only: the up half's), svh [rows].
+ *                             Refusals (exl3_quant.cpp:12-20, 142-247), before any plane is written:
+ *                               UNSUPPORTED  not a routed-expert name; a .bias; half-integer K (last dim 16 K + 8)
+ *                               INVAL        bits outside 2..8, an unknown codebook, a plane missing
+ *                               SHAPE        rows / cols not in 128s (a stacked weight's halves too); a trellis whose
+ *                                            tiles are another [cols, rows]; suh / svh of another dtype or length
+ *                               NOTFOUND     a layer past the layers and the MTP head; a missing trellis, suh or svh
+ *                               DTYPE        a trellis of another K; a marker naming another codebook
+ *                               FORMAT       a trellis not I16 rank 3 or its last dim not in 16s; a marker not an I32
+ *                                            scalar, holding a wrong value, or both markers present
+ *                               IO           a read that failed */
+typedef struct Exl3c4Ckpt Exl3c4Ckpt;
+int     exl3c4_ckpt_open(const char* dir, Exl3c4Ckpt** out);
+void    exl3c4_ckpt_close(Exl3c4Ckpt* ckpt);
+int64_t exl3c4_ckpt_layers(const Exl3c4Ckpt* ckpt);
+int     exl3c4_import_parse_name(const char* name, int32_t* layer, int64_t* expert, int32_t* stacked);
+int     exl3c4_import_weight(Exl3c4Ckpt* ckpt, const char* name, int32_t bits, int32_t codebook, int64_t rows,
+                             int64_t cols, uint8_t* codes, int64_t row_bytes, uint16_t* suh, uint16_t* suh1,
+                             uint16_t* svh);
 
 /* ------------------------------------------------------------------ the plugin rows' instances (checkers' entries)
  * The gate_up_down rows' init hooks return an instance holding a pool of counter blocks, one per (stream, output) pair,

@@ -165,3 +165,31 @@ int exl3c4_unrelayout(const void* record, int64_t rows, int64_t cols, int32_t bi
 #undef URL
     return EXL3C4_OK;
 }
+
+/* exllamav3's tile record -- int16 [cols / 16][rows / 16][16 K], tk outer, a tile its 8 K stream words, each word two
+ * int16 little-endian (common/exl3_layout.c:38-56, common/exl3_decode.c:85-88) -- into the canonical plane: the trellis
+ * tensor of a checkpoint as the import (exl3c4_import.c) takes it. */
+INLINE void record_codes_k(const uint16_t* rec, int64_t rows, int64_t cols, const int bits, uint8_t* codes,
+                           int64_t row_bytes) {
+    uint32_t w[64];
+    const int64_t nt = rows / 16, kt = cols / 16;
+    for (int64_t tk = 0; tk < kt; ++tk)
+        for (int64_t tn = 0; tn < nt; ++tn) {
+            const uint16_t* t = rec + (tk * nt + tn) * 16 * bits;
+            for (int q = 0; q < 8 * bits; ++q) w[q] = (uint32_t)t[2 * q] | ((uint32_t)t[2 * q + 1] << 16);
+            words_tile(w, tk, tn, bits, codes, row_bytes);
+        }
+}
+
+int exl3c4_record_to_codes(const uint16_t* record, int64_t rows, int64_t cols, int32_t bits, uint8_t* codes,
+                           int64_t row_bytes) {
+    if (!codes || !record) return EXL3C4_E_INVAL;
+    if (bits < 1 || bits > 8) return EXL3C4_E_DTYPE;
+    if (rows <= 0 || cols <= 0 || rows % 16 || cols % 16) return EXL3C4_E_SHAPE;
+    if (!row_bytes) row_bytes = (cols * bits + 7) / 8;
+    if (row_bytes < (cols * bits + 7) / 8) return EXL3C4_E_STRIDE;
+#define RC(K) record_codes_k(record, rows, cols, K, codes, row_bytes)
+    BY_K(RC)
+#undef RC
+    return EXL3C4_OK;
+}

@@ -20,7 +20,9 @@ GD_FUSE_MIN_T = 32                  # gate_up_down runs as one kernel at decode 
 CB = {"3inst": 0, "mcg": 1, "mul1": 2}
 F16, BF16 = 0, 1
 STATUS = {0: "OK", -1: "RAD_E_SHAPE", -2: "RAD_E_DTYPE", -3: "RAD_E_ALIGN", -4: "RAD_E_STRIDE", -9: "RAD_E_SCHEMA",
-          -12: "RAD_E_INVAL", -18: "RAD_E_UNSUPPORTED", -20: "RAD_E_SCRATCH", -21: "RAD_E_DEVICE"}
+          -12: "RAD_E_INVAL", -18: "RAD_E_UNSUPPORTED", -20: "RAD_E_SCRATCH", -21: "RAD_E_DEVICE",
+          -5: "RAD_E_FORMAT", -30: "RAD_E_NOTFOUND", -31: "RAD_E_IO"}
+E_FORMAT, E_NOTFOUND, E_IO = -5, -30, -31
 
 _lib = None
 _p = C.c_void_p
@@ -94,6 +96,18 @@ def lib():
         L.exl3c4_launch_gather.argtypes = [C.POINTER(Op), _p, _i64, _p, _p, _i64, _p, _p, _p, _i64]
         L.exl3c4_scratch_status.restype = C.c_int
         L.exl3c4_scratch_status.argtypes = [C.POINTER(Op), C.POINTER(_i64)]
+        L.exl3c4_record_to_codes.restype = C.c_int
+        L.exl3c4_record_to_codes.argtypes = [_p, _i64, _i64, _i32, _p, _i64]
+        L.exl3c4_ckpt_open.restype = C.c_int
+        L.exl3c4_ckpt_open.argtypes = [C.c_char_p, C.POINTER(_p)]
+        L.exl3c4_ckpt_close.restype = None
+        L.exl3c4_ckpt_close.argtypes = [_p]
+        L.exl3c4_ckpt_layers.restype = _i64
+        L.exl3c4_ckpt_layers.argtypes = [_p]
+        L.exl3c4_import_parse_name.restype = C.c_int
+        L.exl3c4_import_parse_name.argtypes = [C.c_char_p, C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_i32)]
+        L.exl3c4_import_weight.restype = C.c_int
+        L.exl3c4_import_weight.argtypes = [_p, C.c_char_p, _i32, _i32, _i64, _i64, _p, _i64, _p, _p, _p]
         L.exl3c4_build_target.restype = C.c_char_p
         L.exl3c4_abi_version.restype = C.c_int
         _lib = L
@@ -119,6 +133,69 @@ def unrelayout(record: np.ndarray, rows: int, cols: int, bits: int) -> np.ndarra
     if rc:
         raise ValueError(f"exl3c4_unrelayout: {STATUS.get(rc, rc)}")
     return out
+
+
+def record_to_codes(record: np.ndarray, rows: int, cols: int, bits: int) -> np.ndarray:
+    """exllamav3's tile record (int16 [cols/16][rows/16][16 K]) -> canonical plane [rows][row_bytes]."""
+    record = np.ascontiguousarray(record).view(np.uint16)
+    rb = (cols * bits + 7) // 8
+    out = np.zeros((rows, rb), np.uint8)
+    rc = lib().exl3c4_record_to_codes(record.ctypes.data, rows, cols, bits, out.ctypes.data, rb)
+    if rc:
+        raise ValueError(f"exl3c4_record_to_codes: {STATUS.get(rc, rc)}")
+    return out
+
+
+# ------------------------------------------------------------------------------------------ the import (host)
+class Checkpoint:
+    """An EXL3 checkpoint directory opened for import (exl3c4_ckpt_open)."""
+
+    def __init__(self, directory: str):
+        self._h = None
+        h = _p()
+        rc = lib().exl3c4_ckpt_open(os.fsencode(directory), C.byref(h))
+        if rc:
+            raise OSError(rc, f"exl3c4_ckpt_open: {STATUS.get(rc, rc)}", directory)
+        self._h = h
+
+    @property
+    def layers(self) -> int:
+        return int(lib().exl3c4_ckpt_layers(self._h))
+
+    def close(self):
+        if self._h:
+            lib().exl3c4_ckpt_close(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    def import_weight_rc(self, name: str, bits: int, cb, rows: int, cols: int, planes: dict) -> int:
+        """exl3c4_import_weight into the caller's planes (numpy: codes uint8 [rows][row_bytes], suh / suh1 uint16 [cols],
+        svh uint16 [rows]; suh1 None for a down weight): the status."""
+        cb = CB[cb] if isinstance(cb, str) else cb
+        codes = planes["codes"]
+        s1 = planes.get("suh1")
+        return lib().exl3c4_import_weight(self._h, name.encode(), bits, cb, rows, cols, codes.ctypes.data,
+                                         codes.shape[1], planes["suh"].ctypes.data,
+                                         None if s1 is None else s1.ctypes.data, planes["svh"].ctypes.data)
+
+    def import_weight(self, name: str, bits: int, cb, rows: int, cols: int) -> dict:
+        """The named routed-expert weight as canonical planes (a status other than OK raises)."""
+        stacked = ".ffn_gate_up_exps." in name
+        planes = {"codes": np.zeros((rows, (cols * bits + 7) // 8), np.uint8), "suh": np.zeros(cols, np.uint16),
+                  "suh1": np.zeros(cols, np.uint16) if stacked else None, "svh": np.zeros(rows, np.uint16)}
+        rc = self.import_weight_rc(name, bits, cb, rows, cols, planes)
+        if rc:
+            raise ValueError(f"exl3c4_import_weight({name}): {STATUS.get(rc, rc)}")
+        return planes
+
+
+def parse_weight_name(name: str):
+    """(layer, expert, stacked) of a routed-expert weight name, or None (exl3c4_import_parse_name)."""
+    layer, expert, stacked = _i32(), _i64(), _i32()
+    rc = lib().exl3c4_import_parse_name(name.encode(), C.byref(layer), C.byref(expert), C.byref(stacked))
+    return None if rc else (layer.value, expert.value, bool(stacked.value))
 
 
 # ------------------------------------------------------------------------------------------ device calls
