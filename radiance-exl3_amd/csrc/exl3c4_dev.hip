@@ -1375,9 +1375,9 @@ __device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, int& unit, 
 
 // One k-step of the prefill GEMM: the step's B operands (decoded just before) against each of the chunk's NT row
 // tiles (4 MFMAs a tile), each group ending in mfma_guard: gfx950 does not interlock a VALU or LDS write against an
-// in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (The MFMAs do not overlap the decode's
-// VALU work anyway -- measured: a mix of both in one wave costs about their sum -- so a step issued behind its
-// decode gains nothing and costs a second set of B registers.)
+// in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (The SIMD already runs one wave's MFMAs
+// under the other waves' decode -- measured about 75-80% hidden with 4 waves a SIMD -- so a step issued behind the
+// next step's decode gained nothing and cost a second set of B registers.)
 template <int BITS, int CB, int NT>
 __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[4][2]) {
     const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
