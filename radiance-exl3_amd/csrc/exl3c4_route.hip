@@ -156,7 +156,14 @@ __device__ __forceinline__ Pick route_token(const void* logits, int64_t row, int
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     uint64_t mykey = 0ull;
     if (n <= 64) {
-        mykey = sort_desc(lane < n ? cand[lane] : 0ull, lane);
+        // the candidates ranked (keys are distinct: the id is in the low bits), then placed by rank: lane r ends with
+        // the r-th largest. n rounds of independent compares instead of a 64-lane sort's 21 dependent stages.
+        const uint64_t ck = lane < n ? cand[lane] : 0ull;
+        int rank = 0;
+        for (int c = 0; c < n; ++c) rank += readlane64(ck, c) > ck ? 1 : 0;
+        if (lane < n) cand[rank] = ck;                            // this wave's row alone: its LDS ops run in order
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        mykey = lane < n ? cand[lane] : 0ull;
     } else {
         uint64_t prev = ~0ull;
         for (int r = 0; r < top_k; ++r) {
@@ -293,11 +300,11 @@ __global__ __launch_bounds__(512) void k_scatter(const int32_t* ids, int32_t T, 
     scatter_body(ids, T, base, n_expert, sorted, off, count, row_of, sc_lds, sc_lds + SC_WAVES * n_expert);
 }
 
-// moe_scatter of at most blockDim.x pairs whose ids sit in LDS (16-byte aligned, room for T rounded up to 4), for
-// at most blockDim.x experts: a histogram (LDS atomics), expert_offset its exclusive scan (a wave scan, then the waves'
-// totals), and pair i's row = offset of its expert + the number of earlier pairs with the same expert (the stable
-// counting sort's row; only the pair threads count, over the ids before theirs, four at a time). lds: n_expert + 1 +
-// 16 ints.
+// moe_scatter of at most blockDim.x pairs whose ids sit in LDS (16-byte aligned; T rounded up to 16 readable, what
+// lies past T read and masked), for at most blockDim.x experts: a histogram (LDS atomics), expert_offset its exclusive
+// scan (a wave scan, then the waves' totals scanned across lanes), and pair i's row = offset of its expert + the
+// number of earlier pairs with the same expert (the stable counting sort's row; only the pair threads count, over the
+// ids before theirs, sixteen at a time). lds: n_expert + 1 + 16 ints.
 __device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int n_expert, int32_t* sorted, int32_t* off,
                                               int32_t* count, int32_t* row_of, int* lds) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -311,9 +318,16 @@ __device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int n
         e = (f >= 0 && f < n_expert) ? f : -1;
         if (e >= 0) {
             atomicAdd(&cnt[e], 1);
-            for (int j0 = 0; j0 < tid; j0 += 4) {                // earlier pairs of the same expert
-                const int4 q = *(const int4*)(ids_l + j0);
-                w += (q.x == e) + (j0 + 1 < tid && q.y == e) + (j0 + 2 < tid && q.z == e) + (j0 + 3 < tid && q.w == e);
+            for (int j0 = 0; j0 < tid; j0 += 16) {               // earlier pairs of the same expert, 16 ids a round:
+                int4 q[4];                                        // four broadcast reads in flight together
+#pragma unroll
+                for (int u = 0; u < 4; ++u) q[u] = *(const int4*)(ids_l + j0 + 4 * u);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int j = j0 + 4 * u;
+                    w += (j < tid && q[u].x == e) + (j + 1 < tid && q[u].y == e) + (j + 2 < tid && q[u].z == e) +
+                         (j + 3 < tid && q[u].w == e);
+                }
             }
         }
     }
@@ -327,12 +341,14 @@ __device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int n
     }
     if (lane == 63) wsum[wv] = incl;
     __syncthreads();
-    int base = 0, live = 0;
-    for (int u = 0; u < (int)(blockDim.x >> 6); ++u) {
-        const int t = wsum[u];
-        base += u < wv ? t : 0;
-        live += t;
+    const int nw = (int)(blockDim.x >> 6);                        // the waves' totals, lane u holding wave u's: an
+    int pre = lane < nw ? wsum[lane] : 0;                         // inclusive scan across lanes (at most 16 waves)
+#pragma unroll
+    for (int d = 1; d < 16; d <<= 1) {
+        const int o = __shfl_up(pre, d);
+        if (lane >= d) pre += o;
     }
+    const int base = wv ? __shfl(pre, wv - 1) : 0, live = __shfl(pre, nw - 1);
     if (tid < n_expert) {
         const int ex = base + incl - c;
         off[tid] = ex;
