@@ -22,8 +22,8 @@ extern "C" {
  * where in a row's line the count of its down units past their wait sits */
 #define EXL3C4_SYNC_STRIDE 64
 #define EXL3C4_SYNC_DONE 32
-/* Rows of one chunk on the prefill path (four MFMA row tiles decode-shared). */
-#define EXL3C4_PF_ROWS 64
+/* Rows of one chunk on the prefill path (six MFMA row tiles share each decoded step). */
+#define EXL3C4_PF_ROWS 96
 /* The prefill plan: PF_PLAN_HDR int32s, then int4 {expert, row0, rows, 0} per chunk. Header: [0] the chunk count;
  * [PF_XCD_GU + x], [PF_XCD_DN + x] (x = 0 .. 8): the first chunk of XCD x for gate_up's and down's GEMM ([.. + 8] = the
  * count). A chunk of t 16-row tiles costs about PF_W_GU + t (gate_up) and PF_W_DN + t (down) units of workgroup time. */

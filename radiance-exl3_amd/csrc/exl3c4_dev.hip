@@ -1331,26 +1331,34 @@ template <int NW> __device__ __forceinline__ void zero_dead_rows(const Exl3c4Lau
 // the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` (>= 1) load and store a
 // copy of the last row: every thread issues the same loads, so the waits the compiler counts for the loads issued
 // before them (the codes in flight) stay exact instead of draining; those rows' products are never written.
-struct StageRegs { u32x4_t v[4]; };
+// The staged input of one 64-k step of a chunk of R = 16 NT rows: R rows x 4 groups of 16 halves, a group two 16-byte
+// loads, spread over 256 threads (H = ceil(R / 64) groups a thread; a slot past the R x 4 groups reloads the last one,
+// so that the loads stay unconditional and their waits exact). Rows past the chunk load a copy of its last row.
+template <int NT> struct StageRegs { u32x4_t v[2 * ((NT + 3) / 4)]; };
+template <int NT>
 __device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, int row0, int nrows, int col0,
-                                           StageRegs& r, int tid = -1) {
-    if (tid < 0) tid = (int)threadIdx.x;
+                                           StageRegs<NT>& r, int tid) {
+    constexpr int H = (NT + 3) / 4, G = 64 * NT;                  // slots a thread, groups a step
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int g = tid + 256 * h;                              // 512 groups: row g / 8, 16-group g % 8
-        const int q = min(g >> 3, nrows - 1), grp = g & 7;
+    for (int h = 0; h < H; ++h) {
+        const int g = min(tid + 256 * h, G - 1);
+        const int q = min(g >> 2, nrows - 1), grp = g & 3;
         const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
             (src + (int64_t)(row0 + q) * pitch + col0 + grp * 16);
         r.v[2 * h] = p[0];
         r.v[2 * h + 1] = p[1];
     }
 }
-__device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs& r, int tid = -1) {
-    if (tid < 0) tid = (int)threadIdx.x;
+// ... and its store into a step buffer [R][kp], each 16-group permuted (kPerm) so that one 16-byte read is the A
+// operand of two MFMAs.
+template <int NT>
+__device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs<NT>& r, int tid) {
+    constexpr int H = (NT + 3) / 4, G = 64 * NT;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < H; ++h) {
         const int g = tid + 256 * h;
-        const int q = g >> 3, grp = g & 7;
+        if (g >= G) break;                                        // uniform in a wave (G is a multiple of 64)
+        const int q = g >> 2, grp = g & 3;
         const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
         u32x4_t* d = (u32x4_t*)(A + q * kp + grp * 16);
         d[0] = u32x4_t{ lo.x, hi.x, lo.y, hi.y };
@@ -1378,8 +1386,9 @@ __device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, int& unit, 
 // in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (The SIMD already runs one wave's MFMAs
 // under the other waves' decode -- measured about 75-80% hidden with 4 waves a SIMD -- so a step issued behind the
 // next step's decode gained nothing and cost a second set of B registers.)
+constexpr int PF_NT = EXL3C4_PF_ROWS / 16;                      // a chunk's row tiles at most
 template <int BITS, int CB, int NT>
-__device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[4][2]) {
+__device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[PF_NT][2]) {
     const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
     const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
 #pragma unroll
@@ -1394,64 +1403,67 @@ __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32
     }
 }
 
-// The prefill GEMM of one chunk (<= 64 rows of one expert) against the strips of one workgroup, all of k: the input's
-// 128-k blocks stream through two LDS buffers a half; each wave decodes its strip's step once and runs it against every
-// row tile (pf_step). NH = 1: 4 waves, one staged input (columns col_off + k). NH = 2: 8
-// waves, two staged inputs (columns k and half_off + k), thread t staging half t / 256 and wave w reading half w / 4.
-// NT: the chunk's 16-row tiles (ceil(nrows / 16)), a template argument so that the loop holds no branch on it.
-// Accumulations: acc[row tile][strip half].
-// The weight: entry jx of the codes table (codes, codes_s) of k = KC columns.
+// The prefill GEMM of one chunk (<= EXL3C4_PF_ROWS rows of one expert) against the strips of one workgroup, all of k:
+// the input streams through two LDS step buffers (64 k each, a half at a time), the next step's loads in flight while
+// this one is multiplied; each wave decodes its strip's step once and runs it against every row tile (pf_step). NH = 1:
+// 4 waves, one staged input (columns col_off + k). NH = 2: 8 waves, two staged inputs (columns k and half_off + k),
+// thread t staging half t / 256 and wave w reading half w / 4. NT: the chunk's 16-row tiles (ceil(nrows / 16)), a
+// template argument so that the loop holds no branch on it and stages only the rows it has. Accumulations:
+// acc[row tile][strip half]. The weight: entry jx of the codes table (codes, codes_s) of k = KC columns.
+constexpr int PF_KP = EXL3C4_KSTEP + 8;                           // a staged row, padded: 16 rows hit 16 bank groups
 template <int BITS, int CB, int NH, int NT>
 __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, int KC, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
-                                        int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
+                                        int half_off, uint16_t* lds, float4_t (&acc)[PF_NT][2]) {
     const int lane = threadIdx.x & 63;
     const int nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
-    const int kp = 128 + 8;
+    constexpr int kp = PF_KP;
     const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
     const int scol = col_off + sh * half_off;                     // this thread's staged input column
-    auto bufp = [&](int b, int h) { return lds + (b * NH + h) * 64 * kp; };
+    auto bufp = [&](int b, int h) { return lds + (b * NH + h) * EXL3C4_PF_ROWS * kp; };
     const gu32p rec = (gu32p)tab_entry(codes, codes_s, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     // the codes of the steps ahead: dA even steps, dB odd; each refill 2 steps ahead of the step it serves (clamped:
     // past the stream a harmless reload of the last step, unconditional so that the waits count exactly)
     uint32_t dA[BITS], dB[BITS];
     load_words<BITS>(rec, dA);
     load_words<BITS>(rec + 64 * BITS, dB);
-    StageRegs r;
-    stage_load(src, pitch, row0, nrows, scol, r, tid);
+    StageRegs<NT> r;
+    stage_load<NT>(src, pitch, row0, nrows, scol, r, tid);
     const Mul1Consts k = mul1_consts();
-    stage_store(bufp(0, sh), kp, r, tid);
+    stage_store<NT>(bufp(0, sh), kp, r, tid);
     __syncthreads();
     const int rr = lane & 15, g = lane >> 4;
     for (int kb = 0; kb < nb; ++kb) {
-        // the next block, or at the last a harmless reload of it: unconditional, like the codes' refills
-        stage_load(src, pitch, row0, nrows, scol + min(kb + 1, nb - 1) * 128, r, tid);
-        const uint16_t* Ab = bufp(kb & 1, sh) + rr * kp + 16 * g;
-        const int ks = 2 * kb;
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
+        for (int s2 = 0; s2 < 2; ++s2) {                          // step ks = 2 kb + s2 sits in buffer s2
+            const int ks = 2 * kb + s2;
+            // the next step, or at the last a harmless reload of it: unconditional, like the codes' refills
+            stage_load<NT>(src, pitch, row0, nrows, scol + min(ks + 1, ksteps - 1) * EXL3C4_KSTEP, r, tid);
             uint32_t B[16];
             decode_segment<BITS, CB>(s2 ? dB : dA, B, k);
-            const int nx = min(ks + s2 + 2, ksteps - 1);
+            const int nx = min(ks + 2, ksteps - 1);
             if (s2 == 0) load_words<BITS>(rec + (int64_t)nx * 64 * BITS, dA);
             else load_words<BITS>(rec + (int64_t)nx * 64 * BITS, dB);
-            pf_step<BITS, CB, NT>(Ab + s2 * EXL3C4_KSTEP, kp, B, acc);
+            pf_step<BITS, CB, NT>(bufp(s2, sh) + rr * kp + 16 * g, kp, B, acc);
+            if (ks + 1 < ksteps) stage_store<NT>(bufp(s2 ^ 1, sh), kp, r, tid);
+            __syncthreads();
         }
-        if (kb + 1 < nb) stage_store(bufp((kb + 1) & 1, sh), kp, r, tid);
-        __syncthreads();
     }
 }
 
 template <int BITS, int CB, int NH>
 __device__ __forceinline__ void pf_gemm(const void* codes, int32_t codes_s, int KC, int64_t jx, int strip,
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
-                                        int half_off, uint16_t* lds, float4_t (&acc)[4][2]) {
+                                        int half_off, uint16_t* lds, float4_t (&acc)[PF_NT][2]) {
 #define EXL3C4_PF_ARGS codes, codes_s, KC, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc
+    static_assert(PF_NT == 6, "pf_gemm instantiates 1 to 6 row tiles");
     switch ((nrows + 15) >> 4) {
     case 1: pf_gemm_nt<BITS, CB, NH, 1>(EXL3C4_PF_ARGS); break;
     case 2: pf_gemm_nt<BITS, CB, NH, 2>(EXL3C4_PF_ARGS); break;
     case 3: pf_gemm_nt<BITS, CB, NH, 3>(EXL3C4_PF_ARGS); break;
-    default: pf_gemm_nt<BITS, CB, NH, 4>(EXL3C4_PF_ARGS); break;
+    case 4: pf_gemm_nt<BITS, CB, NH, 4>(EXL3C4_PF_ARGS); break;
+    case 5: pf_gemm_nt<BITS, CB, NH, 5>(EXL3C4_PF_ARGS); break;
+    default: pf_gemm_nt<BITS, CB, NH, 6>(EXL3C4_PF_ARGS); break;
     }
 #undef EXL3C4_PF_ARGS
 }
@@ -1464,8 +1476,10 @@ __device__ __forceinline__ void pf_gemm(const void* codes, int32_t codes_s, int 
 // narrower class's blocks past its width, are written zero; rows no run holds are the tail workgroups'.
 template <int BITS, int CB>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_gu_pf(const Exl3c4Launch a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * 64 * (128 + 8)];
-    constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [64][256] with padding
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 2 * EXL3C4_PF_ROWS * PF_KP];
+    constexpr int ACC_PITCH = 264;                                // floats: the epilogue's [48][256] with padding
+    constexpr int EPI_T = 3;                                      // row tiles an epilogue pass (48 rows)
+    static_assert(EPI_T * 16 * ACC_PITCH * 4 <= (int)sizeof(lds), "an epilogue pass fits the staging buffers");
     if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // gate_up alone: the rows no run holds
         zero_dead_rows<8>(a, (int)blockIdx.x - a.tail_from);
         return;
@@ -1489,47 +1503,56 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     const int half = wave >> 2, strip = half ? N / 64 + 4 * hb + (wave & 3) : 4 * hb + wave;
-    const int srt = a.sorted[row0 + min(lane, nrows - 1)];        // the chunk's sorted_tok, lane q row q (readlane)
-    float4_t acc[4][2];
+    // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane
+    const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
+    float4_t acc[PF_NT][2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    for (int t = 0; t < PF_NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
     pf_gemm<BITS, CB, 2>(K.codes, K.codes_s, KC, jx, strip, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, KC, lds,
                          acc);
     const int cc = lane & 15, rg = lane >> 4;
     const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
     const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
-    float* acc_l = (float*)lds;                                   // [64][ACC_PITCH], over the staging buffers
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int row = t * 16 + rg * 4 + q;
-            if (row < nrows) {
-                if (a.keep_sums) {
-                    a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
-                    a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
-                }
-                acc_l[row * ACC_PITCH + col_l] = acc[t][0][q];
-                acc_l[row * ACC_PITCH + col_l + 8] = acc[t][1][q];
-            }
-        }
-    __syncthreads();
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
     const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
     const int n0 = hb * 128 + lane, n1 = n0 + 64;
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
     const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
-    for (int row = wave; row < nrows; row += 8) {
-        const int64_t r = row0 + row;
-        uint16_t v0 = 0, v1 = 0;
-        if (__builtin_amdgcn_readlane(srt, row) >= 0) {
-            const float* p = acc_l + row * ACC_PITCH;
-            const float ac[4] = { p[lane], p[lane + 64], p[128 + lane], p[192 + lane] };
-            gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
+    float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
+    // The accumulations cross LDS EPI_T row tiles at a time; each wave then finishes whole rows of the block.
+#pragma unroll
+    for (int p = 0; p < PF_NT / EPI_T; ++p) {
+        const int r0 = p * EPI_T * 16;                            // the pass's first chunk row
+        if (r0 >= nrows) break;                                   // uniform
+        if (p) __syncthreads();                                   // the previous pass's rows are read
+#pragma unroll
+        for (int tt = 0; tt < EPI_T; ++tt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int t = p * EPI_T + tt, row = t * 16 + rg * 4 + q;
+                if (row < nrows) {
+                    if (a.keep_sums) {
+                        a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
+                        a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
+                    }
+                    acc_l[(row - r0) * ACC_PITCH + col_l] = acc[t][0][q];
+                    acc_l[(row - r0) * ACC_PITCH + col_l + 8] = acc[t][1][q];
+                }
+            }
+        __syncthreads();
+        for (int row = r0 + wave; row < min(nrows, r0 + EPI_T * 16); row += 8) {
+            const int64_t r = row0 + row;
+            uint16_t v0 = 0, v1 = 0;
+            const int st = row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64);
+            if (st >= 0) {
+                const float* pp = acc_l + (row - r0) * ACC_PITCH;
+                const float ac[4] = { pp[lane], pp[lane + 64], pp[128 + lane], pp[192 + lane] };
+                gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
+            }
+            uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
+            out[lane] = v0;
+            out[lane + 64] = v1;
         }
-        uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
-        out[lane] = v0;
-        out[lane + 64] = v1;
     }
 }
 
@@ -1538,7 +1561,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 // in its block: a negative sorted_tok and a narrower class's tail as zero; with keep_sums the raw sums to dacc.
 template <int BITS, int CB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void k_dn_pf(const Exl3c4Launch a) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 64 * (128 + 8)];
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * EXL3C4_PF_ROWS * PF_KP];
     if (a.tail_from && (int)blockIdx.x >= a.tail_from) {          // the rows no run holds
         zero_dead_rows<4>(a, (int)blockIdx.x - a.tail_from);
         return;
@@ -1560,10 +1583,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
         return;
     }
-    const int srt = a.sorted[row0 + min(lane, nrows - 1)];        // the chunk's sorted_tok, lane q row q (readlane)
-    float4_t acc[4][2];
+    // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane
+    const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
+    float4_t acc[PF_NT][2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    for (int t = 0; t < PF_NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
     pf_gemm<BITS, CB, 1>(D.codes, D.codes_s, D.cols, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0,
                          lds, acc);
 
@@ -1574,7 +1598,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
     const int ntile = (nrows + 15) >> 4;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {                                 // unrolled: acc[t] stays in registers
+    for (int t = 0; t < PF_NT; ++t) {                             // unrolled: acc[t] stays in registers
         if (t >= ntile) break;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1593,7 +1617,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     dacc[lane + 64] = y1;
                 }
                 uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
-                if (__builtin_amdgcn_readlane(srt, row) < 0) {
+                if ((row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64)) < 0) {
                     out[lane] = 0;
                     out[lane + 64] = 0;
                 } else {

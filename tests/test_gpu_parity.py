@@ -138,11 +138,13 @@ def test_gate_up_down_as_one_kernel_at_the_layer_geometry(torch_cuda):
 
 
 # ------------------------------------------------------------------------------------------ the prefill path
-# (T >= 8 n_expert rows: chunks of up to 64 rows, a plan, the rotation into scratch, the prefill GEMMs)
+# (T >= 8 n_expert rows: chunks of up to 96 rows, a plan, the rotation into scratch, the prefill GEMMs)
 def test_prefill_path_two_classes_several_chunks_with_drops(torch_cuda):
-    case = Case(seed=40, n_tok=96, top_k=2, n_expert=4, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
+    """Runs of 126, 53, 111 and 63 rows: two experts cut into a full 96-row chunk (six row tiles, rows past 64 read
+    their sorted_tok from the second register) and a short one, the others one chunk of 4 tiles."""
+    case = Case(seed=40, n_tok=200, top_k=2, n_expert=4, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
                 drop=0.1, protect_tail=2, routing="zipf")
-    assert case.T >= 8 * case.n_expert and np.diff(case.off).max() > 64
+    assert case.T >= 8 * case.n_expert and np.diff(case.off).max() > 96
     _check_all(case, "prefill two-class")
 
 
