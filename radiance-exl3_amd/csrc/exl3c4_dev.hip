@@ -772,50 +772,44 @@ __device__ __forceinline__ void put_y(const Exl3c4Launch& a, uint16_t* out, int 
 // counts each live row on its token's counter of block b; the count that completes a token (its slots with a row,
 // from row_of) gathers that token's block -- k_gather's sum: the slots in ascending order, one f32 product and one add
 // each, f16 -- over the rows' y read coherently, then sets the counter back to zero. No unit waits here. A chunk holds
-// a token at most once (its slots name distinct experts), at most 16 rows at decode.
+// a token at most once (its slots name distinct experts), at most 16 rows at decode. Wave w takes rows w, w + 4, ..:
+// the row's count and its token's first 16 slots (rows and weights, lane u slot u) go out together, so a completing
+// count finds the slots in registers and the gather's first loads are the rows' y.
 __device__ void gather_count(const Exl3c4Launch& a, int i, int nrows, int b, int tok_l) {
-    __shared__ int tok_s[64];
-    __shared__ int ntok_s;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");              // this thread's y stores are done
-    __syncthreads();
+    __syncthreads();                                              // ... and the workgroup's: the counts may go out
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    if (wave == 0) {
-        bool last = false;
-        int t = -1;
-        if (lane < nrows) {                                       // tok_l: sorted_tok of row i + lane
-            const int p = tok_l;
-            t = p >= 0 ? p / a.top_k : -1;
-            if (t >= 0 && t < a.g_ntok) {
-                const int old = __hip_atomic_fetch_add(a.g_ctr + (int64_t)t * EXL3C4_SYNC_STRIDE + b, 1,
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                // the token's slots with a row (0 <= row < T, as the sum and gather_empty read it), read while the
-                // count is in flight: 16 slots' loads at once (clamped addresses, none behind a branch)
-                int need = 0;
-                for (int s0 = 0; s0 < a.top_k; s0 += 16) {
-                    int r[16];
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) r[u] = a.g_row_of[(int64_t)t * a.top_k + min(s0 + u, a.top_k - 1)];
-#pragma unroll
-                    for (int u = 0; u < 16; ++u) need += (s0 + u < a.top_k && r[u] >= 0 && r[u] < a.T) ? 1 : 0;
-                }
-                last = old == need - 1;
-            }
+    const int K = a.top_k;
+    for (int q = wave; q < nrows; q += 4) {                       // k_gd: 4 waves a workgroup
+        const int p = __builtin_amdgcn_readlane(tok_l, q);        // tok_l: sorted_tok of row i + lane
+        const int64_t t = p >= 0 ? p / K : -1;
+        if (t < 0 || t >= a.g_ntok) continue;
+        int old = 0;
+        if (lane == 0)
+            old = __hip_atomic_fetch_add(a.g_ctr + t * EXL3C4_SYNC_STRIDE + b, 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        // the token's slots with a row (0 <= row < T, as the sum and gather_empty read it), read while the count is
+        // in flight (clamped addresses, none behind a branch)
+        const int sl_l = min(lane & 15, K - 1);
+        const int r_first = a.g_row_of[t * K + sl_l];
+        const float w_first = a.g_w[t * K + sl_l];
+        int need = __popcll(__ballot(lane < 16 && lane < K && r_first >= 0 && r_first < a.T));
+        for (int s0 = 16; s0 < K; s0 += 64) {
+            const int r = a.g_row_of[t * K + min(s0 + lane, K - 1)];
+            need += __popcll(__ballot(s0 + lane < K && r >= 0 && r < a.T));
         }
-        const uint64_t m = __ballot(last);
-        if (last) tok_s[__popcll(m & ((1ull << lane) - 1ull))] = t;
-        if (lane == 0) ntok_s = __popcll(m);
-    }
-    __syncthreads();
-    const int n = ntok_s;
-    for (int j = wave; j < n; j += 4) {                            // k_gd: 4 waves a workgroup
-        const int64_t t = __builtin_amdgcn_readfirstlane(tok_s[j]);   // uniform: the slots' rows and weights in SGPRs
+        if (__builtin_amdgcn_readlane(old, 0) != need - 1) continue;
         const int c = b * 128 + lane;
         float acc0 = 0.f, acc1 = 0.f;
-        for (int s0 = 0; s0 < a.top_k; s0 += 16) {                // 16 slots' rows and weights, then their values
-            // lane u reads slot s0 + u (one round trip for all 16), each then taken uniform by readlane
-            const int sl_l = min(s0 + (lane & 15), a.top_k - 1);
-            const int r_l = a.g_row_of[t * a.top_k + sl_l];
-            const float w_l = a.g_w[t * a.top_k + sl_l];
+        for (int s0 = 0; s0 < K; s0 += 16) {                      // 16 slots' rows and weights, then their values
+            // lane u holds slot s0 + u (the first 16 from the count's loads), each then taken uniform by readlane
+            int r_l = r_first;
+            float w_l = w_first;
+            if (s0 > 0) {
+                const int sl = min(s0 + (lane & 15), K - 1);
+                r_l = a.g_row_of[t * K + sl];
+                w_l = a.g_w[t * K + sl];
+            }
             int r[16];
             float w[16];
             uint16_t q0[16], q1[16];
@@ -914,18 +908,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
     const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_s, jx) : nullptr;
-    if (FUSED) {
-        wait_gate_up(a, i);
-        // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the
-        // row's counters, so a launch leaves them as it found them (the reference's counter blocks,
-        // kernels/exl3r4d/launch.c:311-324)
-        if (threadIdx.x == 0 &&
-            __hip_atomic_fetch_add(row_counter(a, i) + EXL3C4_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                N / 128 - 1) {
-            __hip_atomic_store(row_counter(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(row_counter(a, i) + EXL3C4_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-    }
+    if (FUSED) wait_gate_up(a, i);
 
     // stage the chunk's rows
     const int nhb = KC / 128;
@@ -1000,6 +983,15 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         put_y(a, out, lane, f2bf(y0 * h2f(sv0)), f2bf(y1 * h2f(sv1)));
     }
     if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
+    // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the row's
+    // counters, so a launch leaves them as it found them (the reference's counter blocks,
+    // kernels/exl3r4d/launch.c:311-324). Counted at the unit's end, so that the count's round trip delays no load.
+    if (FUSED && threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(row_counter(a, i) + EXL3C4_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            N / 128 - 1) {
+        __hip_atomic_store(row_counter(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(row_counter(a, i) + EXL3C4_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int BITS, int CB>
