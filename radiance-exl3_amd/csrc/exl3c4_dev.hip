@@ -1029,9 +1029,12 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
 // them forms the chunk's h (row_h) and adds one more; a down unit of that row waits for n_grp x ksplit + 1. The dispatcher deals workgroups to the 8 XCDs in turn and each XCD starts its
 // workgroups in order, so the workgroups g = x (mod 8) share one XCD (its L2 holds the row's sums) and when a down unit
 // runs, every gate_up unit before it has started; gate_up units never wait, so the waits end. The sums cross as
-// coherent accesses (part_ld / part_st), so the bits do not depend on where a workgroup lands.
+// coherent accesses (part_ld / part_st), so the bits do not depend on where a workgroup lands. Built for 7 workgroups
+// a CU up to K = 6 (the register count it holds either way at K = 4; the schedule this target gives measured 0.5 us
+// faster); K = 7, 8 keep the looser target, under which they need no spill.
 template <int BITS, int CB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void k_gd(const Exl3c4Launch a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS <= 6 ? 7 : 5, 8))) void k_gd(
+    const Exl3c4Launch a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
     const int rows = xcd < a.T ? (a.T - 1 - xcd) / 8 + 1 : 0;
@@ -1071,15 +1074,22 @@ __global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
 // (kernels/exl3r4d/launch.c:14-15 clamps the runs); then, for each GEMM, the chunks dealt to the 8 XCDs in contiguous
 // ranges of about equal cost (a chunk of t tiles: W + t; its midpoint in cost order picks the XCD); then each row's
 // owner. Its own kernel (k_plan), or the first workgroup of k_rot's launch, running beside the rotation.
+constexpr int PF_TILES = EXL3C4_PF_ROWS / 16;                     // row tiles a chunk holds at most
+// The plan's chunk order of one GEMM (gate_up 0, down 1): max_chunks entries after the chunk entries.
+__device__ __forceinline__ const int32_t* pf_order(const Exl3c4Launch& a, int gemm) {
+    return a.plan + EXL3C4_PF_PLAN_HDR + 4 * a.max_chunks + gemm * a.max_chunks;
+}
 __device__ __forceinline__ int pf_xcd_of(int p_excl, int cost, int total) {
     return min(7, (int)((8ll * (2ll * p_excl + cost)) / (2ll * max(total, 1))));
 }
 template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& a) {
     __shared__ int scan[NT];
     __shared__ int carry_s, tiles_s, cnt_g[8], cnt_d[8];
+    __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
     const int tid = threadIdx.x;
     if (tid == 0) carry_s = tiles_s = 0;
     if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
+    if (tid < 8 * PF_TILES) cur_g[tid / PF_TILES][tid % PF_TILES] = cur_d[tid / PF_TILES][tid % PF_TILES] = 0;
     __syncthreads();
     int4* ent = (int4*)(a.plan + EXL3C4_PF_PLAN_HDR);
     for (int base = 0; base < a.n_expert; base += NT) {
@@ -1130,8 +1140,13 @@ template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& 
         }
         if (c < nch) {
             const int p = carry + scan[tid] - t;                  // tiles of the chunks before c
-            atomicAdd(&cnt_g[pf_xcd_of(EXL3C4_PF_W_GU * c + p, EXL3C4_PF_W_GU + t, tot_g)], 1);
-            atomicAdd(&cnt_d[pf_xcd_of(EXL3C4_PF_W_DN * c + p, EXL3C4_PF_W_DN + t, tot_d)], 1);
+            const int xg = pf_xcd_of(EXL3C4_PF_W_GU * c + p, EXL3C4_PF_W_GU + t, tot_g);
+            const int xd = pf_xcd_of(EXL3C4_PF_W_DN * c + p, EXL3C4_PF_W_DN + t, tot_d);
+            atomicAdd(&cnt_g[xg], 1);
+            atomicAdd(&cnt_d[xd], 1);
+            atomicAdd(&cur_g[xg][t - 1], 1);
+            atomicAdd(&cur_d[xd][t - 1], 1);
+            ent[c].w = xg | (xd << 8);
         }
         carry += scan[NT - 1];
         __syncthreads();
@@ -1148,6 +1163,27 @@ template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& 
         }
         a.plan[EXL3C4_PF_XCD_GU + 8] = bg;
         a.plan[EXL3C4_PF_XCD_DN + 8] = bd;
+    }
+    // each GEMM's order: inside an XCD's range, chunks of more row tiles first (the longest units start first, so
+    // the range ends on short ones); chunks of equal tiles in any order (where a unit runs changes no bits)
+    if (tid < 16) {
+        int (*cur)[PF_TILES] = tid < 8 ? cur_g : cur_d;
+        const int x = tid & 7;
+        int at = 0;
+        for (int y = 0; y < x; ++y) at += (tid < 8 ? cnt_g : cnt_d)[y];
+        for (int k = PF_TILES - 1; k >= 0; --k) {
+            const int n = cur[x][k];
+            cur[x][k] = at;
+            at += n;
+        }
+    }
+    __syncthreads();
+    int32_t* ord_g = (int32_t*)(ent + a.max_chunks);
+    int32_t* ord_d = ord_g + a.max_chunks;
+    for (int c = tid; c < nch; c += NT) {
+        const int w = ent[c].w, t = (ent[c].z + 15) >> 4;
+        ord_g[atomicAdd(&cur_g[w & 255][t - 1], 1)] = c;
+        ord_d[atomicAdd(&cur_d[w >> 8][t - 1], 1)] = c;
     }
     // each row's owner (row_info[i] = {e or -1, 0}): every row -1 first, then a chunk's rows its expert; the first
     // stores complete before any thread passes the barrier, so a row's last store is its owner's
@@ -1360,17 +1396,20 @@ __device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs
 
 // The prefill GEMMs' workgroups and XCDs: XCD x (the dispatcher deals linear ids g to the XCDs in turn, x = g % 8)
 // takes the plan's contiguous chunk range [xb[x], xb[x + 1]) -- ranges of about equal cost, from k_plan -- its slot
-// g / 8 = per q + u running unit u (0 .. per-1: the chunk's column groups or blocks) of its q-th chunk. A chunk's units
-// run side by side in one L2, so its staged rows come from HBM once; and the plan lists an expert's chunks one after
-// another, so they too share an L2 and, running close in time, read the expert's codes from HBM about once. False
-// for a workgroup with no chunk (the grid covers pf_xcd_bound chunks an XCD). (Where a workgroup lands changes no
-// bits.)
-__device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, int& unit, int& chunk) {
+// g / 8 = per q + u running unit u (0 .. per-1: the chunk's column groups or blocks) of the range's q-th chunk in
+// this GEMM's order (ord: the chunks of more row tiles first, so the range's last units are its shortest). A chunk's
+// units run side by side in one L2, so its staged rows come from HBM once; an expert's chunks fall in one or two
+// ranges, its full chunks side by side in one tile class, so they too share an L2 and, running close in time, read
+// the expert's codes from HBM about once. False for a workgroup with no chunk (the grid covers pf_xcd_bound chunks an
+// XCD). (Where a workgroup lands changes no bits.)
+__device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, const int32_t* ord, int& unit, int& chunk) {
     const int g = (int)blockIdx.x, slot = g >> 3, x = g & 7;
     const int q = slot / per;
     unit = slot - q * per;
-    chunk = xb[x] + q;
-    return chunk < xb[x + 1];
+    const int at = xb[x] + q;
+    if (at >= xb[x + 1]) return false;
+    chunk = ord[at];
+    return true;
 }
 
 // One k-step of the prefill GEMM: the step's B operands (decoded just before) against each of the chunk's NT row
@@ -1477,7 +1516,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     int hb, chunk;
-    if (!xcd_unit(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, hb, chunk)) return;
+    if (!xcd_unit(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, pf_order(a, 0), hb, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
@@ -1559,7 +1598,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     int b, chunk;
-    if (!xcd_unit(a.nblk, a.plan + EXL3C4_PF_XCD_DN, b, chunk)) return;
+    if (!xcd_unit(a.nblk, a.plan + EXL3C4_PF_XCD_DN, pf_order(a, 1), b, chunk)) return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
