@@ -65,30 +65,43 @@ template <int J> __device__ __forceinline__ uint64_t xor_lane64(uint64_t v, int 
 template <int J> __device__ __forceinline__ float xor_lanef(float v, int lane) {
     return __uint_as_float(xor_lane<J>(__float_as_uint(v), lane));
 }
-__device__ __forceinline__ uint64_t xor_lane64_rt(uint64_t v, int j, int lane) {   // j a power of two <= 32
-    switch (j) {
-    case 1: return xor_lane64<1>(v, lane);
-    case 2: return xor_lane64<2>(v, lane);
-    case 4: return xor_lane64<4>(v, lane);
-    case 8: return xor_lane64<8>(v, lane);
-    case 16: return xor_lane64<16>(v, lane);
-    default: return xor_lane64<32>(v, lane);
-    }
-}
 __device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
 }
-// A bitonic sort of one u64 a lane across the wave, descending: lane 0 ends with the largest.
-__device__ __forceinline__ uint64_t sort_desc(uint64_t v, int lane) {
+__device__ __forceinline__ uint32_t xor_lane_rt(uint32_t v, int j, int lane) {   // j a power of two <= 32
+    switch (j) {
+    case 1: return xor_lane<1>(v, lane);
+    case 2: return xor_lane<2>(v, lane);
+    case 4: return xor_lane<4>(v, lane);
+    case 8: return xor_lane<8>(v, lane);
+    case 16: return xor_lane<16>(v, lane);
+    default: return xor_lane<32>(v, lane);
+    }
+}
+
+// A bitonic sort of one u32 a lane across the wave, descending: lane 0 ends with the largest.
+__device__ __forceinline__ uint32_t sort_desc32(uint32_t v, int lane) {
 #pragma unroll
     for (int k = 2; k <= 64; k <<= 1)
 #pragma unroll
         for (int j = k >> 1; j > 0; j >>= 1) {
-            const uint64_t o = xor_lane64_rt(v, j, lane);        // j is a constant once unrolled
+            const uint32_t o = xor_lane_rt(v, j, lane);          // j is a constant once unrolled
             const bool take_max = ((lane & j) == 0) == ((lane & k) == 0);
-            v = take_max ? (o > v ? o : v) : (o < v ? o : v);
+            v = take_max ? max(o, v) : min(o, v);
         }
+    return v;
+}
+
+// The inclusive sum of v over lanes 0 .. lane, by DPP: shifts within each row of 16 lanes, then the rows' totals by
+// row broadcasts (lane 15 into row 1 and 3, lane 31 into rows 2 and 3). Every lane of the wave must be active.
+__device__ __forceinline__ int wave_scan_incl(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15 into rows 1, 3
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31 into rows 2, 3
     return v;
 }
 
@@ -137,17 +150,18 @@ __device__ __forceinline__ Pick route_token(const void* logits, int64_t row, int
     s = s + xor_lanef<2>(s, lane);
     s = s + xor_lanef<1>(s, lane);
 
-    // The top_k keys are all at least thr, the top_k-th largest of the lanes' own largest keys (top_k lanes hold a key
-    // that large). Those candidates -- at most 64 on this path -- are gathered one a lane and sorted; lane r then
-    // holds the r-th ranked key. More than 64 (many equal logits in few lanes) take top_k rounds of a wave maximum.
+    // The top_k keys all have a logit word of at least thr, the top_k-th largest logit word of the lanes' own largest
+    // keys (top_k lanes hold a key that large; the logit word orders the keys, so a 32-bit sort finds it). Those
+    // candidates -- at most 64 on this path -- are gathered one a lane and ranked; lane r then holds the r-th ranked
+    // key. More than 64 (many equal logits in few lanes) take top_k rounds of a wave maximum.
     uint64_t lm = 0ull;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) lm = key[j] > lm ? key[j] : lm;
-    const uint64_t thr = readlane64(sort_desc(lm, lane), top_k - 1);
+    const uint32_t thr = (uint32_t)__builtin_amdgcn_readlane((int)sort_desc32((uint32_t)(lm >> 32), lane), top_k - 1);
     int n = 0;
 #pragma unroll
     for (int j = 0; j < RPL; ++j) {
-        const bool c = key[j] != 0ull && key[j] >= thr;
+        const bool c = key[j] != 0ull && (uint32_t)(key[j] >> 32) >= thr;
         const uint64_t bal = __ballot(c);
         const int at = n + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
         if (c && at < 64) cand[at] = key[j];
@@ -300,60 +314,38 @@ __global__ __launch_bounds__(512) void k_scatter(const int32_t* ids, int32_t T, 
     scatter_body(ids, T, base, n_expert, sorted, off, count, row_of, sc_lds, sc_lds + SC_WAVES * n_expert);
 }
 
-// moe_scatter of at most blockDim.x pairs whose ids sit in LDS (16-byte aligned; T rounded up to 16 readable, what
-// lies past T read and masked), for at most blockDim.x experts: a histogram (LDS atomics), expert_offset its exclusive
-// scan (a wave scan, then the waves' totals scanned across lanes), and pair i's row = offset of its expert + the
-// number of earlier pairs with the same expert (the stable counting sort's row; only the pair threads count, over the
-// ids before theirs, sixteen at a time). lds: n_expert + 1 + 16 ints.
-__device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int n_expert, int32_t* sorted, int32_t* off,
-                                              int32_t* count, int32_t* row_of, int* lds) {
+// moe_scatter of the router's pairs (token t's top_k ids at t * top_k .., distinct experts, at most 32 tokens and
+// blockDim.x pairs) for at most blockDim.x experts: each expert's set of tokens as a bit mask (LDS atomics), its count
+// the mask's population; expert_offset the counts' exclusive scan (a DPP scan in each wave, then the waves' totals
+// scanned the same way); pair (t, slot)'s row = offset of its expert + the number of earlier tokens holding that
+// expert (the stable counting sort's row: a token holds an expert at most once, so the pairs of one expert are in
+// token order). lds: n_expert + 1 + 16 ints, the first n_expert zeroed by the caller before a barrier.
+__device__ __forceinline__ void scatter_small(const int32_t* ids_l, int T, int top_k, int n_expert, int32_t* sorted,
+                                              int32_t* off, int32_t* count, int32_t* row_of, int* lds) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    int* cnt = lds;                                               // [n_expert]: counts, then exclusive offsets
+    int* cnt = lds;                                               // [n_expert]: token masks, then exclusive offsets
     int* wsum = lds + n_expert + 1;                               // [16]: the waves' totals
-    if (tid < n_expert) cnt[tid] = 0;
-    __syncthreads();
     int e = -1, w = 0;
+    const int t = tid < T ? tid / top_k : 0;
     if (tid < T) {
         const int f = ids_l[tid];
         e = (f >= 0 && f < n_expert) ? f : -1;
-        if (e >= 0) {
-            atomicAdd(&cnt[e], 1);
-            for (int j0 = 0; j0 < tid; j0 += 16) {               // earlier pairs of the same expert, 16 ids a round:
-                int4 q[4];                                        // four broadcast reads in flight together
-#pragma unroll
-                for (int u = 0; u < 4; ++u) q[u] = *(const int4*)(ids_l + j0 + 4 * u);
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int j = j0 + 4 * u;
-                    w += (j < tid && q[u].x == e) + (j + 1 < tid && q[u].y == e) + (j + 2 < tid && q[u].z == e) +
-                         (j + 3 < tid && q[u].w == e);
-                }
-            }
-        }
+        if (e >= 0) atomicOr((unsigned*)&cnt[e], 1u << t);
     }
     __syncthreads();
-    const int c = tid < n_expert ? cnt[tid] : 0;
-    int incl = c;                                                 // inclusive scan across the wave
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(incl, d);
-        if (lane >= d) incl += o;
-    }
+    const int c = tid < n_expert ? __popc((unsigned)cnt[tid]) : 0;
+    if (e >= 0) w = __popc((unsigned)cnt[e] & ((1u << t) - 1u));  // read before any offset overwrites a mask
+    const int incl = wave_scan_incl(c);                           // inclusive scan across the wave
     if (lane == 63) wsum[wv] = incl;
     __syncthreads();
-    const int nw = (int)(blockDim.x >> 6);                        // the waves' totals, lane u holding wave u's: an
-    int pre = lane < nw ? wsum[lane] : 0;                         // inclusive scan across lanes (at most 16 waves)
-#pragma unroll
-    for (int d = 1; d < 16; d <<= 1) {
-        const int o = __shfl_up(pre, d);
-        if (lane >= d) pre += o;
-    }
-    const int base = wv ? __shfl(pre, wv - 1) : 0, live = __shfl(pre, nw - 1);
+    const int nw = (int)(blockDim.x >> 6);                        // the waves' totals, lane u holding wave u's,
+    const int pre = wave_scan_incl(lane < nw ? wsum[lane] : 0);   // scanned across lanes (at most 16 waves)
+    const int base = wv ? __builtin_amdgcn_readlane(pre, wv - 1) : 0, live = __builtin_amdgcn_readlane(pre, nw - 1);
     if (tid < n_expert) {
         const int ex = base + incl - c;
         off[tid] = ex;
         if (count) count[tid] = c;
-        cnt[tid] = ex;                                            // this thread alone read cnt[tid] above
+        cnt[tid] = ex;                                            // every read of the masks lies before the barrier
     }
     if (tid == 0) off[n_expert] = live;
     __syncthreads();
@@ -377,6 +369,9 @@ __global__ __launch_bounds__(1024) void k_route_scatter(const void* logits, int3
     int* ids_l = rs_lds;                                          // [16 * 64]
     int* cnt = rs_lds + 16 * 64;
     const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
+    const bool small = n_tok <= 32 && n_tok * top_k <= (int)blockDim.x && n_expert <= (int)blockDim.x;
+    if (small)                                                    // the histogram's counts, zeroed while routing
+        for (int i = threadIdx.x; i < n_expert; i += blockDim.x) cnt[i] = 0;
     if (t < n_tok) {
         const Pick p = route_token<DT, RPL>(logits, (int64_t)t * pitch, n_expert, top_k, renorm, lane, cand[t]);
         if (lane < top_k) {
@@ -386,8 +381,7 @@ __global__ __launch_bounds__(1024) void k_route_scatter(const void* logits, int3
         }
     }
     __syncthreads();
-    if (n_tok * top_k <= (int)blockDim.x && n_expert <= (int)blockDim.x)
-        scatter_small(ids_l, n_tok * top_k, n_expert, sorted, off, count, row_of, cnt);
+    if (small) scatter_small(ids_l, n_tok * top_k, top_k, n_expert, sorted, off, count, row_of, cnt);
     else scatter_body(ids_l, n_tok * top_k, 0, n_expert, sorted, off, count, row_of, cnt, cnt + SC_WAVES * n_expert);
 }
 
