@@ -416,7 +416,11 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
     out[lane + 64] = o1;
 }
 
-__device__ __forceinline__ float silu(float g) { return g * (1.0f / (1.0f + expf(-g))); }
+// silu(g) = g / (1 + e^-g) as g x rcp(1 + exp2(-g log2 e)): the hardware exp2 and reciprocal (4 instructions against
+// 26 for expf and an IEEE division), within a few f32 ulps of the reference's g * (1 / (1 + expf(-g)))
+// (kernels/exl3ref/ref.c:187-212) -- below the f16 rounding of silu(gate) * up that follows, which the reference
+// value then meets within one f16 ulp. The same function on every path, so the paths' bits agree.
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // A partial sum as gate_up_down's single kernel exchanges it between workgroups: a relaxed atomic access at agent
 // scope, coherent across the XCDs' L2 caches by itself (ordered by the row counter: the writer waits for its stores
