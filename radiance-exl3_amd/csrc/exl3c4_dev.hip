@@ -68,34 +68,34 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-// round to nearest even on the f32 bits (radiance's rad_f32_to_bf16); a nan stays a quiet nan
-__device__ __forceinline__ uint16_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7FFFu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// Two f32 to bf16 (lo in the low half): round to nearest even on the f32 bits, a nan kept quiet as (u >> 16) | 0x40
+// (radiance's rad_f32_to_bf16). One v_cvt_pk_bf16_f32 (gfx950), which gives those bits for every f32: compared on
+// the device over each of the 65,536 upper halves with the low halves 0, 1, 0x7FFF, 0x8000, 0x8001 and 0xFFFF (every
+// nan class, the ties, the denormals) and 4 M random values, without a difference.
+__device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){ lo, hi }, bf16x2_t));
 }
 
-// The normalised Sylvester Hadamard over one 128-block held by a wave, lane l holding x[l] (v0) and x[l + 64] (v1):
-// the butterfly stages h = 1 .. 64 in the reference's order, each (a + b) low and (a - b) high in f32, then one f32
-// multiply by 1/sqrt(128) (common/exl3_decode.c:172-189) -- the same roundings, so the same bits.
+// The element of a 128-block that lane l holds for the Hadamard (v0; v1 holds that + 64): l with bits 0 and 1
+// flipped where bit 2 is set. Then the partners of every stage up to h = 8 are DPP lanes: element j ^ 1, j ^ 2 at
+// lane l ^ 1, l ^ 2 (quad_perm), j ^ 4 at l ^ 7 (row_half_mirror), j ^ 8 at l ^ 8 (row_ror 8). Every kernel loads,
+// scales and stores a block's values at these elements, so the map changes no value.
+__device__ __forceinline__ int had_col(int lane) { return lane ^ (((lane >> 2) & 1) * 3); }
+
+// The normalised Sylvester Hadamard over one 128-block held by a wave, lane l holding x[j] (v0) and x[j + 64] (v1),
+// j = had_col(l): the butterfly stages h = 1 .. 64 in the reference's order, each (a + b) low and (a - b) high in f32,
+// then one f32 multiply by 1/sqrt(128) (common/exl3_decode.c:172-189) -- the same roundings, so the same bits.
 // Each stage is one fused multiply-add by +-1 (exact product, one rounding: the same value as the add or the
-// subtract). For h = 1, 2, 8 it is one v_fmac_f32 whose partner operand comes by DPP (quad_perm, row_ror 8): v += c p
-// with c = -1 on the lanes whose bit h is set, which leaves those lanes the NEGATED result (v - p = -(p - v)); the
-// partner of a lane has the same lower bits, hence the same sign, so c needs no correction, and the signs are undone
-// by the final multiply (by -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of the lane are set). h = 4:
-// the partner is l - 4 (row_ror 4) when bit 2 of l is set, else l + 4 (row_ror 12); both moves sit in one asm block
-// so that neither can be sunk under a partial exec mask, where a DPP read of an inactive lane is void. h = 16, 32:
-// gfx950's permlane swaps leave each lane the pair's low-half value and its high-half value, v = lo + c up.
+// subtract). For h = 1, 2, 4, 8 it is one v_fmac_f32 whose partner operand comes by DPP: v += c p with c = -1 where
+// bit h of j is set, which leaves those lanes the NEGATED result (v - p = -(p - v)); a partner's element has the
+// same lower bits, hence the same sign, so c needs no correction, and the signs are undone by the final multiply (by
+// -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of j are set). h = 16, 32: gfx950's permlane swaps leave
+// each lane the pair's low-half value and its high-half value, v = lo + c up. The DPP stages run with the whole wave
+// active: every caller's branch around them is uniform.
 #define HAD_DPP(v, c, CTRL) asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:0xf bank_mask:0xf" \
                                          : "+v"(v) : "v"(c))
-__device__ __forceinline__ float partner4(float v, bool hi) {
-    float a, b;
-    asm volatile("s_nop 1\n\tv_mov_b32_dpp %0, %2 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
-                 "v_mov_b32_dpp %1, %2 row_ror:12 row_mask:0xf bank_mask:0xf"
-                 : "=&v"(a), "=&v"(b) : "v"(v));
-    return hi ? a : b;
-}
 template <int H> __device__ __forceinline__ void bfly_swap(float& v, float c) {
     const unsigned u = __builtin_bit_cast(unsigned, v);
     unsigned lo_u, up_u;
@@ -109,15 +109,15 @@ template <int H> __device__ __forceinline__ void bfly_swap(float& v, float c) {
     v = fmaf(c, __builtin_bit_cast(float, up_u), __builtin_bit_cast(float, lo_u));
 }
 __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
-    const float c1 = (lane & 1) ? -1.f : 1.f, c2 = (lane & 2) ? -1.f : 1.f, c4 = (lane & 4) ? -1.f : 1.f;
-    const float c8 = (lane & 8) ? -1.f : 1.f, c16 = (lane & 16) ? -1.f : 1.f, c32 = (lane & 32) ? -1.f : 1.f;
+    const int j = had_col(lane);
+    const float c1 = (j & 1) ? -1.f : 1.f, c2 = (j & 2) ? -1.f : 1.f, c4 = (j & 4) ? -1.f : 1.f;
+    const float c8 = (j & 8) ? -1.f : 1.f, c16 = (j & 16) ? -1.f : 1.f, c32 = (j & 32) ? -1.f : 1.f;
     HAD_DPP(v0, c1, "quad_perm:[1,0,3,2]");
     HAD_DPP(v1, c1, "quad_perm:[1,0,3,2]");
     HAD_DPP(v0, c2, "quad_perm:[2,3,0,1]");
     HAD_DPP(v1, c2, "quad_perm:[2,3,0,1]");
-    const bool hi4 = lane & 4;
-    v0 = fmaf(partner4(v0, hi4), c4, v0);
-    v1 = fmaf(partner4(v1, hi4), c4, v1);
+    HAD_DPP(v0, c4, "row_half_mirror");
+    HAD_DPP(v1, c4, "row_half_mirror");
     HAD_DPP(v0, c8, "row_ror:8");
     HAD_DPP(v1, c8, "row_ror:8");
     bfly_swap<16>(v0, c16);
@@ -125,7 +125,7 @@ __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
     bfly_swap<32>(v0, c32);
     bfly_swap<32>(v1, c32);
     const float a = v0 + v1, b = v0 - v1;
-    const float sc = (__builtin_popcount(lane & 15) & 1) ? -kHadScale : kHadScale;
+    const float sc = (__builtin_popcount(j & 15) & 1) ? -kHadScale : kHadScale;
     v0 = a * sc;
     v1 = b * sc;
 }
@@ -357,7 +357,8 @@ __device__ __forceinline__ int chunk_rows(const Exl3c4Launch& a, const Owner& w,
 // products are never written) read the last staged row, so no read leaves the workgroup's LDS.
 __device__ __forceinline__ int a_row(const Exl3c4Launch& a, int lane) { return min(lane & 15, a.chunk_rows - 1); }
 
-// f16(had128(f16(v * s))) over one 128-block, lane l holding k = l (0) and l + 64 (1) (kernels/exl3ref/ref.c:27-32).
+// f16(had128(f16(v * s))) over one 128-block, lane l holding k = had_col(l) (0) and + 64 (1) (kernels/exl3ref/
+// ref.c:27-32).
 __device__ __forceinline__ void rotate_block(float f0, float f1, uint16_t s0, uint16_t s1, int lane, uint16_t& o0,
                                              uint16_t& o1) {
     float v0 = h2f(f2h(f0 * h2f(s0))), v1 = h2f(f2h(f1 * h2f(s1)));
@@ -381,7 +382,7 @@ __device__ __forceinline__ void lds_put(uint16_t* A, int q, int kp, int col0, in
 // (m = 1) of the row's expert. Rows outside every run are not written (include/exl3_abi.h:273-278); a run's row whose
 // sorted_tok is negative is written zero.
 __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, el = had_col(lane);
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int nb = a.x_cols_max / 128;
     if (wid >= (int64_t)a.T * 2 * nb) return;
@@ -407,13 +408,13 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
     src = src < a.x_rows ? src : a.x_rows - 1;
     const void* x = (const uint16_t*)a.x + src * a.x_pitch + b * 128;
     const void* s = m ? tab_entry(K.suh1, K.suh1_s, jx) : tab_entry(K.suh, K.suh_s, jx);
-    const uint16_t x0 = ldg16(x, lane), x1 = ldg16(x, 64 + lane);
+    const uint16_t x0 = ldg16(x, el), x1 = ldg16(x, 64 + el);
     const float f0 = a.x_dtype == EXL3C4_BF16 ? bf2f(x0) : h2f(x0);
     const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
     uint16_t o0, o1;
-    rotate_block(f0, f1, ldg16(s, b * 128 + lane), ldg16(s, b * 128 + 64 + lane), lane, o0, o1);
-    out[lane] = o0;
-    out[lane + 64] = o1;
+    rotate_block(f0, f1, ldg16(s, b * 128 + el), ldg16(s, b * 128 + 64 + el), lane, o0, o1);
+    out[el] = o0;
+    out[el + 64] = o1;
 }
 
 // silu(g) = g / (1 + e^-g) as g x rcp(1 + exp2(-g log2 e)): the hardware exp2 and reciprocal (4 instructions against
@@ -469,8 +470,8 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
     }
 }
 
-// gate_up's epilogue on one 128-column block of a row, lane l holding gate columns l, l + 64 (acc[0], acc[1]) and up
-// columns l, l + 64 (acc[2], acc[3]) of the block's f32 sums, svh of those four columns and (h_rot) dn_suh of the two:
+// gate_up's epilogue on one 128-column block of a row, lane l holding gate columns j, j + 64 (acc[0], acc[1]) and up
+// columns j, j + 64 (acc[2], acc[3]) of the block's f32 sums (j = had_col(l)), svh of those four columns and (h_rot) dn_suh of the two:
 // had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))).
 __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0, uint16_t sg1, uint16_t su0,
                                              uint16_t su1, uint16_t d0, uint16_t d1, int h_rot, int lane,
@@ -496,13 +497,13 @@ __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0
 
 // gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
 // sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
-// values for columns b * 128 + l (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
+// values for columns b * 128 + had_col(l) (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
 // 187-212).
 template <bool COH>
 __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4DevClass& K, int64_t i, int b,
                                               int64_t jx, int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
-    const int n0 = b * 128 + lane, n1 = n0 + 64;
+    const int n0 = b * 128 + had_col(lane), n1 = n0 + 64;
     const int width = K.rows / 2;
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
     const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
@@ -578,7 +579,7 @@ template <int BITS, bool AROT>
 __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows, int KC, bool up, int b0, int b1,
                                          int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
                                          uint16_t* A, int kp) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, el = had_col(lane);
     constexpr int GU_WB = 4;
     const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
     const bool bf = a.x_dtype == EXL3C4_BF16;
@@ -594,15 +595,15 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
         uint16_t x0[GU_WB], x1[GU_WB];
 #pragma unroll
         for (int j = 0; j < GU_WB; ++j) {
-            x0[j] = ldg16(xr, hbj[j] * 128 + lane);
-            x1[j] = ldg16(xr, hbj[j] * 128 + 64 + lane);
+            x0[j] = ldg16(xr, hbj[j] * 128 + el);
+            x1[j] = ldg16(xr, hbj[j] * 128 + 64 + el);
         }
         if (q == 0) {                        // then the codes' first steps and the scales: one round trip for all
             prime<BITS>(rec, ksn, ring);
 #pragma unroll
             for (int j = 0; j < GU_WB; ++j) {
-                s0[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + lane);
-                s1[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + 64 + lane);
+                s0[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + el);
+                s1[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + 64 + el);
             }
         }
 #pragma unroll
@@ -615,17 +616,17 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
                     rotate_block(bf ? bf2f(x0[j]) : h2f(x0[j]), bf ? bf2f(x1[j]) : h2f(x1[j]), s0[j], s1[j], lane, v0,
                                  v1);
             }
-            lds_put(A, q, kp, (hbj[j] - b0) * 128, lane, v0, v1);
+            lds_put(A, q, kp, (hbj[j] - b0) * 128, el, v0, v1);
         }
         for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
-            const uint16_t y0 = ldg16(xr, hb * 128 + lane), y1 = ldg16(xr, hb * 128 + 64 + lane);
-            const uint16_t t0 = AROT ? 0 : ldg16(sv, hb * 128 + lane), t1 = AROT ? 0 : ldg16(sv, hb * 128 + 64 + lane);
+            const uint16_t y0 = ldg16(xr, hb * 128 + el), y1 = ldg16(xr, hb * 128 + 64 + el);
+            const uint16_t t0 = AROT ? 0 : ldg16(sv, hb * 128 + el), t1 = AROT ? 0 : ldg16(sv, hb * 128 + 64 + el);
             uint16_t v0 = y0, v1 = y1;
             if (!AROT) {
                 v0 = v1 = 0;
                 if (tok >= 0) rotate_block(bf ? bf2f(y0) : h2f(y0), bf ? bf2f(y1) : h2f(y1), t0, t1, lane, v0, v1);
             }
-            lds_put(A, q, kp, (hb - b0) * 128, lane, v0, v1);
+            lds_put(A, q, kp, (hb - b0) * 128, el, v0, v1);
         }
     }
 }
@@ -703,7 +704,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 // gate_up's epilogue (gate_up alone): one wave per (sorted row i, 128-column block b) of h, from the partial sums.
 // A row no run holds, a negative sorted_tok and a narrower class's tail are written zero.
 __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63;
+    const int lane = threadIdx.x & 63, el = had_col(lane);
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int per = max(1, a.blk_per_wave), nw = (a.nblk + per - 1) / per;   // a wave takes `per` blocks of a row
     if (wid >= (int64_t)a.T * nw) return;
@@ -717,8 +718,8 @@ __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
         uint16_t v0 = 0, v1 = 0;
         if (!dead && b * 128 < a.cls[c].rows / 2)
             gate_up_block<false>(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
-        out[lane] = v0;
-        out[lane + 64] = v1;
+        out[el] = v0;
+        out[el + 64] = v1;
     }
 }
 
@@ -910,7 +911,8 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     CodeRing<BITS> ring;
     prime<BITS>(rec, ksteps, ring);
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
-    const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
+    const int el = had_col(lane);                                // this lane's elements of the block
+    const uint16_t sv0 = ldg16(svh, b * 128 + el), sv1 = ldg16(svh, b * 128 + 64 + el);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_s, jx) : nullptr;
     if (FUSED) wait_gate_up(a, i);
 
@@ -935,22 +937,22 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
             uint16_t v0 = 0, v1 = 0;
             if (FUSED) {                                          // the row's h, formed once (row_h)
                 const uint16_t* hs = a.hbuf + r * a.hbuf_pitch + hb * 128;
-                v0 = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                v1 = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v0 = __hip_atomic_load(hs + el, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v1 = __hip_atomic_load(hs + el + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else if (a.h_from_gu) {
                 if (a.sorted[r] >= 0) gate_up_block<false>(a, a.cls[c], r, hb, jx, 1, lane, v0, v1);
             } else {
                 const void* xs = (const uint16_t*)a.x + r * a.x_pitch + hb * 128;
-                const uint16_t x0 = ldg16(xs, lane), x1 = ldg16(xs, lane + 64);
+                const uint16_t x0 = ldg16(xs, el), x1 = ldg16(xs, el + 64);
                 if (a.h_rot) {
                     v0 = x0;
                     v1 = x1;
                 } else {
-                    rotate_block(h2f(x0), h2f(x1), ldg16(suh, hb * 128 + lane), ldg16(suh, hb * 128 + 64 + lane), lane,
+                    rotate_block(h2f(x0), h2f(x1), ldg16(suh, hb * 128 + el), ldg16(suh, hb * 128 + 64 + el), lane,
                                  v0, v1);
                 }
             }
-            lds_put(A, q, kp, hb * 128, lane, v0, v1);
+            lds_put(A, q, kp, hb * 128, el, v0, v1);
         }
     }
     __syncthreads();
@@ -974,17 +976,18 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
 
     for (int q = wave; q < nrows; q += 4) {
         const int64_t r = i + q;
-        float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
+        float y0 = acc_l[q * 128 + el], y1 = acc_l[q * 128 + el + 64];
         float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
-        dacc[lane] = y0;
-        dacc[lane + 64] = y1;
+        dacc[el] = y0;
+        dacc[el + 64] = y1;
         uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
         if (__builtin_amdgcn_readlane(tok_l, q) < 0) {
-            put_y(a, out, lane, 0, 0);
+            put_y(a, out, el, 0, 0);
             continue;
         }
         had128_wave(y0, y1, lane);
-        put_y(a, out, lane, f2bf(y0 * h2f(sv0)), f2bf(y1 * h2f(sv1)));
+        const uint32_t yb = f2bf2(y0 * h2f(sv0), y1 * h2f(sv1));
+        put_y(a, out, el, (uint16_t)yb, (uint16_t)(yb >> 16));
     }
     if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
     // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the row's
@@ -1007,7 +1010,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) voi
 // h of a chunk's rows (gate_up's epilogue with h_rot: had128, x svh, f16(silu(gate) * up), f16(had(f16(h * dn_suh))))
 // from the rows' partial sums, once, by the row's last gate_up unit: into hbuf, then one more count on row i's counter.
 __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows& g) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, el = had_col(lane);
     const int c = class_of(a, g.e);
     const int64_t jx = entry_of(a, g.e);
     const Exl3c4DevClass& G = a.cls[c];
@@ -1019,8 +1022,8 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
         gate_up_block<true>(a, G, r, hb, jx, 1, lane, v0, v1);
         if (a.sorted[r] < 0) v0 = v1 = 0;
         uint16_t* h = a.hbuf + r * a.hbuf_pitch + hb * 128;
-        __hip_atomic_store(h + lane, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(h + lane + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(h + el, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(h + el + 64, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -1550,7 +1553,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
     const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
-    const int n0 = hb * 128 + lane, n1 = n0 + 64;
+    const int el = had_col(lane), n0 = hb * 128 + el, n1 = n0 + 64;
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
     const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
     float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
@@ -1581,12 +1584,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             const int st = row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64);
             if (st >= 0) {
                 const float* pp = acc_l + (row - r0) * ACC_PITCH;
-                const float ac[4] = { pp[lane], pp[lane + 64], pp[128 + lane], pp[192 + lane] };
+                const float ac[4] = { pp[el], pp[el + 64], pp[128 + el], pp[192 + el] };
                 gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
             }
             uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
-            out[lane] = v0;
-            out[lane + 64] = v1;
+            out[el] = v0;
+            out[el + 64] = v1;
         }
     }
 }
@@ -1627,7 +1630,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                          lds, acc);
 
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
-    const uint16_t sv0 = ldg16(svh, b * 128 + lane), sv1 = ldg16(svh, b * 128 + 64 + lane);
+    const int el = had_col(lane);                                // this lane's elements of the block
+    const uint16_t sv0 = ldg16(svh, b * 128 + el), sv1 = ldg16(svh, b * 128 + 64 + el);
     float* acc_l = (float*)lds;                                   // [16][128], one row tile at a time
     const int cc = lane & 15, rg = lane >> 4;
     const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
@@ -1645,20 +1649,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             const int row = t * 16 + q;
             if (row < nrows) {
                 const int64_t r = row0 + row;
-                float y0 = acc_l[q * 128 + lane], y1 = acc_l[q * 128 + lane + 64];
+                float y0 = acc_l[q * 128 + el], y1 = acc_l[q * 128 + el + 64];
                 if (a.keep_sums) {
                     float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
-                    dacc[lane] = y0;
-                    dacc[lane + 64] = y1;
+                    dacc[el] = y0;
+                    dacc[el + 64] = y1;
                 }
                 uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
                 if ((row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64)) < 0) {
-                    out[lane] = 0;
-                    out[lane + 64] = 0;
+                    out[el] = 0;
+                    out[el + 64] = 0;
                 } else {
                     had128_wave(y0, y1, lane);
-                    out[lane] = f2bf(y0 * h2f(sv0));
-                    out[lane + 64] = f2bf(y1 * h2f(sv1));
+                    const uint32_t yb = f2bf2(y0 * h2f(sv0), y1 * h2f(sv1));
+                    out[el] = (uint16_t)yb;
+                    out[el + 64] = (uint16_t)(yb >> 16);
                 }
             }
         }
