@@ -80,38 +80,51 @@ __device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {
 
 // The element of a 128-block that lane l holds for the Hadamard (v0; v1 holds that + 64): l with bits 0 and 1
 // flipped where bit 2 is set. Then the partners of every stage up to h = 8 are DPP lanes: element j ^ 1, j ^ 2 at
-// lane l ^ 1, l ^ 2 (quad_perm), j ^ 4 at l ^ 7 (row_half_mirror), j ^ 8 at l ^ 8 (row_ror 8). Every kernel loads,
-// scales and stores a block's values at these elements, so the map changes no value.
+// lane l ^ 1, l ^ 2 (quad_perm), j ^ 4 at l ^ 7 (row_half_mirror), j ^ 8 at l ^ 8 (row_ror 8). had128_wave<false>
+// takes a block in this layout and leaves it in had_col_t's (bits 4 and 5 of the element exchanged), and
+// had128_wave<true> the other way round. Every kernel loads, scales and stores a block's values at the elements of
+// its layout, so the maps change no value.
 __device__ __forceinline__ int had_col(int lane) { return lane ^ (((lane >> 2) & 1) * 3); }
+__device__ __forceinline__ int had_col_t(int lane) {
+    const int j = had_col(lane);
+    return (j & ~48) | ((j & 16) << 1) | ((j & 32) >> 1);
+}
 
-// The normalised Sylvester Hadamard over one 128-block held by a wave, lane l holding x[j] (v0) and x[j + 64] (v1),
-// j = had_col(l): the butterfly stages h = 1 .. 64 in the reference's order, each (a + b) low and (a - b) high in f32,
-// then one f32 multiply by 1/sqrt(128) (common/exl3_decode.c:172-189) -- the same roundings, so the same bits.
-// Each stage is one fused multiply-add by +-1 (exact product, one rounding: the same value as the add or the
-// subtract). For h = 1, 2, 4, 8 it is one v_fmac_f32 whose partner operand comes by DPP: v += c p with c = -1 where
-// bit h of j is set, which leaves those lanes the NEGATED result (v - p = -(p - v)); a partner's element has the
-// same lower bits, hence the same sign, so c needs no correction, and the signs are undone by the final multiply (by
-// -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of j are set). h = 16, 32: gfx950's permlane swaps leave
-// each lane the pair's low-half value and its high-half value, v = lo + c up. The DPP stages run with the whole wave
-// active: every caller's branch around them is uniform.
+// The normalised Sylvester Hadamard over one 128-block held by a wave: the butterfly stages h = 1 .. 64 in the
+// reference's order, each (a + b) low and (a - b) high in f32, then one f32 multiply by 1/sqrt(128)
+// (common/exl3_decode.c:172-189) -- the same roundings, so the same bits. Bits 0..3 of an element sit in bits 0..3 of
+// its lane (had_col); bits 4, 5 and 6 in lane bit 4, lane bit 5 and the register (v0, v1), in an order each stage
+// from h = 16 on changes. For h = 1, 2, 4, 8 the stage is one v_fmac_f32 whose partner operand comes by DPP:
+// v += c p with c = -1 where bit h of the element is set, which leaves those lanes the NEGATED result
+// (v - p = -(p - v)); a partner's element has the same lower bits, hence the same sign, so c needs no correction,
+// and the signs are undone by the final multiply (by -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of the
+// element are set). For h = 16, 32, 64 one permlane swap of v0 and v1 (gfx950: VDST's odd 16-lane rows with
+// SRC0's even rows, or VDST's upper 32 lanes with SRC0's lower ones) brings the stage's bit from the lane into the
+// register, so the pair sits in one lane and the stage is an add and a subtract; the bit the register held goes to
+// the lane. The DPP and swap stages run with the whole wave active: every caller's branch around them is uniform.
 #define HAD_DPP(v, c, CTRL) asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:0xf bank_mask:0xf" \
                                          : "+v"(v) : "v"(c))
-template <int H> __device__ __forceinline__ void bfly_swap(float& v, float c) {
-    const unsigned u = __builtin_bit_cast(unsigned, v);
-    unsigned lo_u, up_u;
-    if constexpr (H == 16) {
-        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-        lo_u = r[0]; up_u = r[1];
+// v0 and v1 exchanged across 16-lane rows (W = 16) or 32-lane halves (W = 32): a lane of the odd row (upper half)
+// takes the partner lane's v1 into its v0, a lane of the even row (lower half) its partner's v0 into its v1.
+template <int W> __device__ __forceinline__ void swap_rows(float& v0, float& v1) {
+    const unsigned a = __builtin_bit_cast(unsigned, v0), b = __builtin_bit_cast(unsigned, v1);
+    unsigned na, nb;
+    if constexpr (W == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        na = r[0]; nb = r[1];
     } else {
-        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-        lo_u = r[0]; up_u = r[1];
+        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+        na = r[0]; nb = r[1];
     }
-    v = fmaf(c, __builtin_bit_cast(float, up_u), __builtin_bit_cast(float, lo_u));
+    v0 = __builtin_bit_cast(float, na);
+    v1 = __builtin_bit_cast(float, nb);
 }
-__device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
-    const int j = had_col(lane);
+// T_IN = false: in had_col's layout (element bits 4, 5, 6 in lane bit 4, lane bit 5, the register), out in
+// had_col_t's (lane bit 5, lane bit 4, the register); T_IN = true the other way round.
+template <bool T_IN> __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
+    const int j = had_col(lane);                                  // the element's bits 0..3, in either layout
     const float c1 = (j & 1) ? -1.f : 1.f, c2 = (j & 2) ? -1.f : 1.f, c4 = (j & 4) ? -1.f : 1.f;
-    const float c8 = (j & 8) ? -1.f : 1.f, c16 = (j & 16) ? -1.f : 1.f, c32 = (j & 32) ? -1.f : 1.f;
+    const float c8 = (j & 8) ? -1.f : 1.f;
     HAD_DPP(v0, c1, "quad_perm:[1,0,3,2]");
     HAD_DPP(v1, c1, "quad_perm:[1,0,3,2]");
     HAD_DPP(v0, c2, "quad_perm:[2,3,0,1]");
@@ -120,11 +133,20 @@ __device__ __forceinline__ void had128_wave(float& v0, float& v1, int lane) {
     HAD_DPP(v1, c4, "row_half_mirror");
     HAD_DPP(v0, c8, "row_ror:8");
     HAD_DPP(v1, c8, "row_ror:8");
-    bfly_swap<16>(v0, c16);
-    bfly_swap<16>(v1, c16);
-    bfly_swap<32>(v0, c32);
-    bfly_swap<32>(v1, c32);
-    const float a = v0 + v1, b = v0 - v1;
+    float a, b;
+    swap_rows<T_IN ? 32 : 16>(v0, v1);                            // h = 16: bit 4 into the register
+    a = v0 + v1;
+    b = v0 - v1;
+    v0 = a;
+    v1 = b;
+    swap_rows<T_IN ? 16 : 32>(v0, v1);                            // h = 32: bit 5 into the register
+    a = v0 + v1;
+    b = v0 - v1;
+    v0 = a;
+    v1 = b;
+    swap_rows<T_IN ? 32 : 16>(v0, v1);                            // h = 64: bit 6 back into the register
+    a = v0 + v1;
+    b = v0 - v1;
     const float sc = (__builtin_popcount(j & 15) & 1) ? -kHadScale : kHadScale;
     v0 = a * sc;
     v1 = b * sc;
@@ -357,12 +379,12 @@ __device__ __forceinline__ int chunk_rows(const Exl3c4Launch& a, const Owner& w,
 // products are never written) read the last staged row, so no read leaves the workgroup's LDS.
 __device__ __forceinline__ int a_row(const Exl3c4Launch& a, int lane) { return min(lane & 15, a.chunk_rows - 1); }
 
-// f16(had128(f16(v * s))) over one 128-block, lane l holding k = had_col(l) (0) and + 64 (1) (kernels/exl3ref/
-// ref.c:27-32).
+// f16(had128(f16(v * s))) over one 128-block, lane l holding k = had_col(l) (0) and + 64 (1) of v and s, and
+// leaving k = had_col_t(l) and + 64 of the result (kernels/exl3ref/ref.c:27-32).
 __device__ __forceinline__ void rotate_block(float f0, float f1, uint16_t s0, uint16_t s1, int lane, uint16_t& o0,
                                              uint16_t& o1) {
     float v0 = h2f(f2h(f0 * h2f(s0))), v1 = h2f(f2h(f1 * h2f(s1)));
-    had128_wave(v0, v1, lane);
+    had128_wave<false>(v0, v1, lane);
     o0 = f2h(v0);
     o1 = f2h(v1);
 }
@@ -413,8 +435,9 @@ __global__ __launch_bounds__(256) void k_prep(const Exl3c4Launch a) {
     const float f1 = a.x_dtype == EXL3C4_BF16 ? bf2f(x1) : h2f(x1);
     uint16_t o0, o1;
     rotate_block(f0, f1, ldg16(s, b * 128 + el), ldg16(s, b * 128 + 64 + el), lane, o0, o1);
-    out[el] = o0;
-    out[el + 64] = o1;
+    const int et = had_col_t(lane);
+    out[et] = o0;
+    out[et + 64] = o1;
 }
 
 // silu(g) = g / (1 + e^-g) as g x rcp(1 + exp2(-g log2 e)): the hardware exp2 and reciprocal (4 instructions against
@@ -471,14 +494,15 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
 }
 
 // gate_up's epilogue on one 128-column block of a row, lane l holding gate columns j, j + 64 (acc[0], acc[1]) and up
-// columns j, j + 64 (acc[2], acc[3]) of the block's f32 sums (j = had_col(l)), svh of those four columns and (h_rot) dn_suh of the two:
-// had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))).
+// columns j, j + 64 (acc[2], acc[3]) of the block's f32 sums (j = had_col(l)), and svh and (h_rot) dn_suh of the
+// columns t, t + 64 (t = had_col_t(l)): had128, x svh, f16(silu(gate) * up), and with h_rot down's first step
+// f16(had(f16(h * dn_suh))). The result is h's columns t, t + 64 without h_rot, j, j + 64 with it.
 __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0, uint16_t sg1, uint16_t su0,
                                              uint16_t su1, uint16_t d0, uint16_t d1, int h_rot, int lane,
                                              uint16_t& v0, uint16_t& v1) {
     float g0 = acc[0], g1 = acc[1], u0 = acc[2], u1 = acc[3];
-    had128_wave(g0, g1, lane);
-    had128_wave(u0, u1, lane);
+    had128_wave<false>(g0, g1, lane);
+    had128_wave<false>(u0, u1, lane);
     g0 = g0 * h2f(sg0);
     g1 = g1 * h2f(sg1);
     u0 = u0 * h2f(su0);
@@ -490,24 +514,25 @@ __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0
         return;
     }
     float r0 = h2f(f2h(h2f(h0) * h2f(d0))), r1 = h2f(f2h(h2f(h1) * h2f(d1)));
-    had128_wave(r0, r1, lane);
+    had128_wave<true>(r0, r1, lane);
     v0 = f2h(r0);
     v1 = f2h(r1);
 }
 
 // gate_up's output for one 128-column block b of sorted row i (class geometry K, table entry jx), from its partial
 // sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
-// values for columns b * 128 + had_col(l) (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
+// values for columns b * 128 + (h_rot ? had_col(l) : had_col_t(l)) (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
 // 187-212).
 template <bool COH>
 __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4DevClass& K, int64_t i, int b,
                                               int64_t jx, int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
-    const int n0 = b * 128 + had_col(lane), n1 = n0 + 64;
+    const int n0 = b * 128 + had_col(lane), n1 = n0 + 64;        // the sums' columns
+    const int t0 = b * 128 + had_col_t(lane), t1 = t0 + 64;      // the scales' columns
     const int width = K.rows / 2;
-    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
+    const uint16_t sg0 = ldg16(svh, t0), sg1 = ldg16(svh, t1), su0 = ldg16(svh, width + t0), su1 = ldg16(svh, width + t1);
     const void* ds = h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
-    const uint16_t d0 = h_rot ? ldg16(ds, n0) : 0, d1 = h_rot ? ldg16(ds, n1) : 0;
+    const uint16_t d0 = h_rot ? ldg16(ds, t0) : 0, d1 = h_rot ? ldg16(ds, t1) : 0;
     const int col[4] = { n0, n1, width + n0, width + n1 };
     float acc[4];
     sum_splits4<COH>(a, i, col, acc);
@@ -580,6 +605,7 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
                                          int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
                                          uint16_t* A, int kp) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, el = had_col(lane);
+    const int eo = AROT ? el : had_col_t(lane);                   // where a staged value goes
     constexpr int GU_WB = 4;
     const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
     const bool bf = a.x_dtype == EXL3C4_BF16;
@@ -616,7 +642,7 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
                     rotate_block(bf ? bf2f(x0[j]) : h2f(x0[j]), bf ? bf2f(x1[j]) : h2f(x1[j]), s0[j], s1[j], lane, v0,
                                  v1);
             }
-            lds_put(A, q, kp, (hbj[j] - b0) * 128, el, v0, v1);
+            lds_put(A, q, kp, (hbj[j] - b0) * 128, eo, v0, v1);
         }
         for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
             const uint16_t y0 = ldg16(xr, hb * 128 + el), y1 = ldg16(xr, hb * 128 + 64 + el);
@@ -626,7 +652,7 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
                 v0 = v1 = 0;
                 if (tok >= 0) rotate_block(bf ? bf2f(y0) : h2f(y0), bf ? bf2f(y1) : h2f(y1), t0, t1, lane, v0, v1);
             }
-            lds_put(A, q, kp, (hb - b0) * 128, el, v0, v1);
+            lds_put(A, q, kp, (hb - b0) * 128, eo, v0, v1);
         }
     }
 }
@@ -704,7 +730,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 // gate_up's epilogue (gate_up alone): one wave per (sorted row i, 128-column block b) of h, from the partial sums.
 // A row no run holds, a negative sorted_tok and a narrower class's tail are written zero.
 __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
-    const int lane = threadIdx.x & 63, el = had_col(lane);
+    const int lane = threadIdx.x & 63, el = a.h_rot ? had_col(lane) : had_col_t(lane);  // h's columns
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int per = max(1, a.blk_per_wave), nw = (a.nblk + per - 1) / per;   // a wave takes `per` blocks of a row
     if (wid >= (int64_t)a.T * nw) return;
@@ -911,8 +937,8 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     CodeRing<BITS> ring;
     prime<BITS>(rec, ksteps, ring);
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
-    const int el = had_col(lane);                                // this lane's elements of the block
-    const uint16_t sv0 = ldg16(svh, b * 128 + el), sv1 = ldg16(svh, b * 128 + 64 + el);
+    const int el = had_col(lane), et = had_col_t(lane);          // the block's sums' columns, its outputs'
+    const uint16_t sv0 = ldg16(svh, b * 128 + et), sv1 = ldg16(svh, b * 128 + 64 + et);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_s, jx) : nullptr;
     if (FUSED) wait_gate_up(a, i);
 
@@ -935,6 +961,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         const int64_t r = i + q;
         for (int hb = wave; hb < nhb; hb += 4) {
             uint16_t v0 = 0, v1 = 0;
+            int ep = el;                                          // where the staged values go
             if (FUSED) {                                          // the row's h, formed once (row_h)
                 const uint16_t* hs = a.hbuf + r * a.hbuf_pitch + hb * 128;
                 v0 = __hip_atomic_load(hs + el, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -950,9 +977,10 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
                 } else {
                     rotate_block(h2f(x0), h2f(x1), ldg16(suh, hb * 128 + el), ldg16(suh, hb * 128 + 64 + el), lane,
                                  v0, v1);
+                    ep = et;
                 }
             }
-            lds_put(A, q, kp, hb * 128, el, v0, v1);
+            lds_put(A, q, kp, hb * 128, ep, v0, v1);
         }
     }
     __syncthreads();
@@ -985,9 +1013,9 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
             put_y(a, out, el, 0, 0);
             continue;
         }
-        had128_wave(y0, y1, lane);
+        had128_wave<false>(y0, y1, lane);
         const uint32_t yb = f2bf2(y0 * h2f(sv0), y1 * h2f(sv1));
-        put_y(a, out, el, (uint16_t)yb, (uint16_t)(yb >> 16));
+        put_y(a, out, et, (uint16_t)yb, (uint16_t)(yb >> 16));
     }
     if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
     // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the row's
@@ -1456,6 +1484,8 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
     const int lane = threadIdx.x & 63;
     const int nb = KC / 128, ksteps = KC / EXL3C4_KSTEP;
     constexpr int kp = PF_KP;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };   // the chunk's tiles only
     const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
     const int scol = col_off + sh * half_off;                     // this thread's staged input column
     auto bufp = [&](int b, int h) { return lds + (b * NH + h) * EXL3C4_PF_ROWS * kp; };
@@ -1471,7 +1501,8 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
     stage_store<NT>(bufp(0, sh), kp, r, tid);
     __syncthreads();
     const int rr = lane & 15, g = lane >> 4;
-    for (int kb = 0; kb < nb; ++kb) {
+    int kb = 0;
+    do {                                                          // nb >= 1: the launch checks refuse k of 0
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {                          // step ks = 2 kb + s2 sits in buffer s2
             const int ks = 2 * kb + s2;
@@ -1486,7 +1517,7 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
             if (ks + 1 < ksteps) stage_store<NT>(bufp(s2 ^ 1, sh), kp, r, tid);
             __syncthreads();
         }
-    }
+    } while (++kb < nb);
 }
 
 template <int BITS, int CB, int NH>
@@ -1543,9 +1574,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int half = wave >> 2, strip = half ? N / 64 + 4 * hb + (wave & 3) : 4 * hb + wave;
     // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane
     const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
-    float4_t acc[PF_NT][2];
-#pragma unroll
-    for (int t = 0; t < PF_NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    float4_t acc[PF_NT][2];                                       // pf_gemm zeroes the chunk's tiles
     pf_gemm<BITS, CB, 2>(K.codes, K.codes_s, KC, jx, strip, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, KC, lds,
                          acc);
     const int cc = lane & 15, rg = lane >> 4;
@@ -1553,7 +1582,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
     const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
-    const int el = had_col(lane), n0 = hb * 128 + el, n1 = n0 + 64;
+    const int el = had_col(lane), n0 = hb * 128 + had_col_t(lane), n1 = n0 + 64;   // the scales' columns
+    const int eo = a.h_rot ? el : had_col_t(lane);                                  // h's columns
     const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
     const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
     float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
@@ -1588,8 +1618,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
             }
             uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
-            out[el] = v0;
-            out[el + 64] = v1;
+            out[eo] = v0;
+            out[eo + 64] = v1;
         }
     }
 }
@@ -1623,15 +1653,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
     // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane
     const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
-    float4_t acc[PF_NT][2];
-#pragma unroll
-    for (int t = 0; t < PF_NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+    float4_t acc[PF_NT][2];                                       // pf_gemm zeroes the chunk's tiles
     pf_gemm<BITS, CB, 1>(D.codes, D.codes_s, D.cols, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0,
                          lds, acc);
 
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
-    const int el = had_col(lane);                                // this lane's elements of the block
-    const uint16_t sv0 = ldg16(svh, b * 128 + el), sv1 = ldg16(svh, b * 128 + 64 + el);
+    const int el = had_col(lane), et = had_col_t(lane);          // the block's sums' columns, its outputs'
+    const uint16_t sv0 = ldg16(svh, b * 128 + et), sv1 = ldg16(svh, b * 128 + 64 + et);
     float* acc_l = (float*)lds;                                   // [16][128], one row tile at a time
     const int cc = lane & 15, rg = lane >> 4;
     const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
@@ -1660,10 +1688,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     out[el] = 0;
                     out[el + 64] = 0;
                 } else {
-                    had128_wave(y0, y1, lane);
+                    had128_wave<false>(y0, y1, lane);
                     const uint32_t yb = f2bf2(y0 * h2f(sv0), y1 * h2f(sv1));
-                    out[el] = (uint16_t)yb;
-                    out[el + 64] = (uint16_t)(yb >> 16);
+                    out[et] = (uint16_t)yb;
+                    out[et + 64] = (uint16_t)(yb >> 16);
                 }
             }
         }
