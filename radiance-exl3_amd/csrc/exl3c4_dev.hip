@@ -957,6 +957,45 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
 #pragma unroll
         for (int q = 0; q < R; ++q)
             if (q < nrows && hb < nhb) lds_put(A, q, kp, hb * 128, lane, h0[q], h1[q]);
+    } else if (!FUSED && !a.h_from_gu) {                          // down's input rows (its op's, or h from k_gepi):
+        // each of a wave's blocks with every row's loads first, none behind a branch (rows past the chunk load its
+        // last, unused): a block costs one round trip, not one a row
+        for (int hb = wave; hb < nhb; hb += 4) {                  // uniform in the wave
+            if (a.h_rot) {                                        // as given: columns 2 l, 2 l + 1 a lane, one dword
+                constexpr int R = EXL3C4_CHUNK_ROWS;              // (they are adjacent in the permuted layout too)
+                uint32_t h[R];
+#pragma unroll
+                for (int q = 0; q < R; ++q) {
+                    const uint16_t* xs = (const uint16_t*)a.x + (int64_t)(i + min(q, nrows - 1)) * a.x_pitch + hb * 128;
+                    h[q] = *(const __attribute__((address_space(1))) uint32_t*)(xs + 2 * lane);
+                }
+                const int o = perm_slot(2 * lane);
+#pragma unroll
+                for (int q = 0; q < R; ++q)
+                    if (q < nrows) *(uint32_t*)(A + q * kp + hb * 128 + o) = h[q];
+            } else {                                              // rotated here: f16(had128(f16(x * suh)))
+                constexpr int R = EXL3C4_CHUNK_ROWS / 2;          // eight rows' loads at a time
+                const uint16_t s0 = ldg16(suh, hb * 128 + el), s1 = ldg16(suh, hb * 128 + 64 + el);
+                for (int q0 = 0; q0 < nrows; q0 += R) {
+                    uint16_t h0[R], h1[R];
+#pragma unroll
+                    for (int q = 0; q < R; ++q) {
+                        const uint16_t* xs =
+                            (const uint16_t*)a.x + (int64_t)(i + min(q0 + q, nrows - 1)) * a.x_pitch + hb * 128;
+                        h0[q] = ldg16(xs, el);
+                        h1[q] = ldg16(xs, el + 64);
+                    }
+#pragma unroll
+                    for (int q = 0; q < R; ++q) {
+                        if (q0 + q < nrows) {                     // uniform: the rotation's DPP runs the whole wave
+                            uint16_t v0, v1;
+                            rotate_block(h2f(h0[q]), h2f(h1[q]), s0, s1, lane, v0, v1);
+                            lds_put(A, q0 + q, kp, hb * 128, et, v0, v1);
+                        }
+                    }
+                }
+            }
+        }
     } else for (int q = 0; q < nrows; ++q) {
         const int64_t r = i + q;
         for (int hb = wave; hb < nhb; hb += 4) {
