@@ -593,66 +593,54 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r
     }
 }
 
-// gate_up's staging of a split's input rows in LDS (the split's 128-blocks [b0, b1), wave w taking hb = b0 + w + 4 j):
-// as given (AROT: x holds the rotated rows, the gate half then the up half) or f16(had128(f16(x * s))) of the row's
-// token (s = suh or suh1, zero for a negative sorted_tok). Up to GU_WB blocks of the wave have their scale and input
-// loads issued together, a row at a time, none of them behind a branch (addresses clamped: a block past the split
-// loads the split's last one, unused), so a row costs one memory round trip; wider splits take the rest one block at
-// a time. The first row's input, the codes' first steps and the scales go out together (one round trip); the codes
-// are not waited for before the loop.
+// gate_up's staging of a split's input rows in LDS (the split's 128-blocks [b0, b1)): as given (AROT: x holds the
+// rotated rows, the gate half then the up half) or f16(had128(f16(x * s))) of the row's token (s = suh or suh1, zero
+// for a negative sorted_tok). The (row, block) pairs of the chunk, row-major, are dealt to the four waves, GU_PB a wave
+// a round: a round's input and scale loads all go out before any is used, none behind a branch (a pair past the last
+// loads the last, unused), so a round costs one memory round trip however its pairs fall over rows and blocks (a chunk
+// of 16 rows and one block: one round, not 16 round trips in series). The codes' first steps go out right after the
+// first round's inputs, so they are in flight while it is staged; the codes are not waited for before the loop.
 template <int BITS, bool AROT>
 __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows, int KC, bool up, int b0, int b1,
                                          int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
                                          uint16_t* A, int kp) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, el = had_col(lane);
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63, el = had_col(lane);
     const int eo = AROT ? el : had_col_t(lane);                   // where a staged value goes
-    constexpr int GU_WB = 4;
-    const int nbw = b1 - b0 > wave ? (b1 - b0 - wave + 3) / 4 : 0;
+    constexpr int GU_PB = 4;
+    const int nbs = b1 - b0, npair = nrows * nbs;
     const bool bf = a.x_dtype == EXL3C4_BF16;
-    int hbj[GU_WB];
-    uint16_t s0[GU_WB], s1[GU_WB];
+    for (int p0 = 0; p0 < npair; p0 += 4 * GU_PB) {
+        int q[GU_PB], hb[GU_PB], tok[GU_PB];
+        uint16_t x0[GU_PB], x1[GU_PB], s0[GU_PB], s1[GU_PB];
 #pragma unroll
-    for (int j = 0; j < GU_WB; ++j) hbj[j] = min(b0 + wave + 4 * j, b1 - 1);
-    for (int q = 0; q < nrows; ++q) {
-        const int tok = AROT ? 0 : __builtin_amdgcn_readlane(tok_l, q);
-        int64_t src = AROT ? (int64_t)i + q : (tok >= 0 ? tok / a.top_k : 0);
-        src = src < a.x_rows ? src : a.x_rows - 1;
-        const uint16_t* xr = (const uint16_t*)a.x + src * a.x_pitch + (AROT && up ? KC : 0);
-        uint16_t x0[GU_WB], x1[GU_WB];
-#pragma unroll
-        for (int j = 0; j < GU_WB; ++j) {
-            x0[j] = ldg16(xr, hbj[j] * 128 + el);
-            x1[j] = ldg16(xr, hbj[j] * 128 + 64 + el);
+        for (int j = 0; j < GU_PB; ++j) {                         // wave-uniform: the pair's row and block
+            const int pc = min(p0 + wave + 4 * j, npair - 1);
+            q[j] = pc / nbs;
+            hb[j] = b0 + (pc - q[j] * nbs);
+            tok[j] = AROT ? 0 : __builtin_amdgcn_readlane(tok_l, q[j]);
+            int64_t src = AROT ? (int64_t)i + q[j] : (tok[j] >= 0 ? tok[j] / a.top_k : 0);
+            src = src < a.x_rows ? src : a.x_rows - 1;
+            const uint16_t* xr = (const uint16_t*)a.x + src * a.x_pitch + (AROT && up ? KC : 0);
+            x0[j] = ldg16(xr, hb[j] * 128 + el);
+            x1[j] = ldg16(xr, hb[j] * 128 + 64 + el);
         }
-        if (q == 0) {                        // then the codes' first steps and the scales: one round trip for all
-            prime<BITS>(rec, ksn, ring);
+        if (p0 == 0) prime<BITS>(rec, ksn, ring);
 #pragma unroll
-            for (int j = 0; j < GU_WB; ++j) {
-                s0[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + el);
-                s1[j] = AROT ? 0 : ldg16(sv, hbj[j] * 128 + 64 + el);
-            }
+        for (int j = 0; j < GU_PB; ++j) {
+            s0[j] = AROT ? 0 : ldg16(sv, hb[j] * 128 + el);
+            s1[j] = AROT ? 0 : ldg16(sv, hb[j] * 128 + 64 + el);
         }
 #pragma unroll
-        for (int j = 0; j < GU_WB; ++j) {
-            if (j >= nbw) break;
+        for (int j = 0; j < GU_PB; ++j) {
+            if (p0 + wave + 4 * j >= npair) break;                // uniform: the rotation's DPP runs the whole wave
             uint16_t v0 = x0[j], v1 = x1[j];
             if (!AROT) {
                 v0 = v1 = 0;
-                if (tok >= 0)
+                if (tok[j] >= 0)
                     rotate_block(bf ? bf2f(x0[j]) : h2f(x0[j]), bf ? bf2f(x1[j]) : h2f(x1[j]), s0[j], s1[j], lane, v0,
                                  v1);
             }
-            lds_put(A, q, kp, (hbj[j] - b0) * 128, eo, v0, v1);
-        }
-        for (int hb = b0 + wave + 4 * GU_WB; hb < b1; hb += 4) {
-            const uint16_t y0 = ldg16(xr, hb * 128 + el), y1 = ldg16(xr, hb * 128 + 64 + el);
-            const uint16_t t0 = AROT ? 0 : ldg16(sv, hb * 128 + el), t1 = AROT ? 0 : ldg16(sv, hb * 128 + 64 + el);
-            uint16_t v0 = y0, v1 = y1;
-            if (!AROT) {
-                v0 = v1 = 0;
-                if (tok >= 0) rotate_block(bf ? bf2f(y0) : h2f(y0), bf ? bf2f(y1) : h2f(y1), t0, t1, lane, v0, v1);
-            }
-            lds_put(A, q, kp, (hb - b0) * 128, eo, v0, v1);
+            lds_put(A, q[j], kp, (hb[j] - b0) * 128, eo, v0, v1);
         }
     }
 }
