@@ -459,8 +459,27 @@ template <bool COH> __device__ __forceinline__ void part_st(float* p, float v) {
 }
 
 // The split-K partial sums of four columns of sorted row i, added in ascending split order (the order fixes the
-// bits). The loads go out four splits at a time (16 registers), so S / 4 round trips in all.
-template <bool COH>
+// bits). The loads go out R splits at a time (4 R registers): S / R round trips in all. R = min(S, SR), SR the
+// caller's budget of registers (4, 8 or 16 splits).
+template <bool COH, int R>
+__device__ __forceinline__ void sum_rounds(const __attribute__((address_space(1))) float* p, int S, int64_t st,
+                                           const int (&col)[4], float (&out)[4]) {
+    for (int q0 = 0; q0 < S; q0 += R) {                           // S is a multiple of R (both powers of two)
+        float v[4][R];
+#pragma unroll
+        for (int q = 0; q < R; ++q)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) v[c][q] = part_ld<COH>(p + (int64_t)(q0 + q) * st + col[c]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float t = q0 == 0 ? v[c][0] : out[c] + v[c][0];
+#pragma unroll
+            for (int q = 1; q < R; ++q) t = t + v[c][q];
+            out[c] = t;
+        }
+    }
+}
+template <bool COH, int SR = 4>
 __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, const int (&col)[4], float (&out)[4]) {
     const __attribute__((address_space(1))) float* p =
         (const __attribute__((address_space(1))) float*)a.part + i * a.part_pitch;
@@ -477,20 +496,9 @@ __device__ __forceinline__ void sum_splits4(const Exl3c4Launch& a, int64_t i, co
         for (int c = 0; c < 4; ++c) out[c] = S == 2 ? v[c][0] + v[c][1] : v[c][0];
         return;
     }
-    for (int q0 = 0; q0 < S; q0 += 4) {
-        float v[4][4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) v[c][q] = part_ld<COH>(p + (int64_t)(q0 + q) * st + col[c]);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            float t = q0 == 0 ? v[c][0] : out[c] + v[c][0];
-            t = t + v[c][1];
-            t = t + v[c][2];
-            out[c] = t + v[c][3];
-        }
-    }
+    if (SR >= 16 && S >= 16) sum_rounds<COH, (SR >= 16 ? 16 : 4)>(p, S, st, col, out);
+    else if (SR >= 8 && S >= 8) sum_rounds<COH, (SR >= 8 ? 8 : 4)>(p, S, st, col, out);
+    else sum_rounds<COH, 4>(p, S, st, col, out);
 }
 
 // gate_up's epilogue on one 128-column block of a row, lane l holding gate columns j, j + 64 (acc[0], acc[1]) and up
@@ -523,7 +531,7 @@ __device__ __forceinline__ void gate_up_math(const float (&acc)[4], uint16_t sg0
 // sums: had128, x svh, f16(silu(gate) * up), and with h_rot down's first step f16(had(f16(h * dn_suh))) -- lane l's
 // values for columns b * 128 + (h_rot ? had_col(l) : had_col_t(l)) (v0) and + 64 (v1), as fp16 bits (docs/OPS-exl3.md:104-123; kernels/exl3ref/ref.c:
 // 187-212).
-template <bool COH>
+template <bool COH, int SR = 4>
 __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c4DevClass& K, int64_t i, int b,
                                               int64_t jx, int h_rot, int lane, uint16_t& v0, uint16_t& v1) {
     const void* svh = tab_entry(K.svh, K.svh_s, jx);
@@ -535,7 +543,7 @@ __device__ __forceinline__ void gate_up_block(const Exl3c4Launch& a, const Exl3c
     const uint16_t d0 = h_rot ? ldg16(ds, t0) : 0, d1 = h_rot ? ldg16(ds, t1) : 0;
     const int col[4] = { n0, n1, width + n0, width + n1 };
     float acc[4];
-    sum_splits4<COH>(a, i, col, acc);
+    sum_splits4<COH, SR>(a, i, col, acc);
     gate_up_math(acc, sg0, sg1, su0, su1, d0, d1, h_rot, lane, v0, v1);
 }
 
@@ -717,6 +725,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6, 8))) voi
 
 // gate_up's epilogue (gate_up alone): one wave per (sorted row i, 128-column block b) of h, from the partial sums.
 // A row no run holds, a negative sorted_tok and a narrower class's tail are written zero.
+// SR: split-K sums loaded a round (8 for S >= 8, the launches of few rows: one round trip where S = 16 took four).
+template <int SR>
 __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
     const int lane = threadIdx.x & 63, el = a.h_rot ? had_col(lane) : had_col_t(lane);  // h's columns
     const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -731,7 +741,7 @@ __global__ __launch_bounds__(256) void k_gepi(const Exl3c4Launch a) {
         uint16_t* out = (uint16_t*)a.y + i * a.y_pitch + b * 128;
         uint16_t v0 = 0, v1 = 0;
         if (!dead && b * 128 < a.cls[c].rows / 2)
-            gate_up_block<false>(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
+            gate_up_block<false, SR>(a, a.cls[c], i, b, entry_of(a, e), a.h_rot, lane, v0, v1);
         out[el] = v0;
         out[el + 64] = v1;
     }
@@ -1853,7 +1863,8 @@ extern "C" int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, v
     const int per = a->blk_per_wave > 0 ? a->blk_per_wave : 1;
     const int64_t waves = (int64_t)a->T * ((a->nblk + per - 1) / per);
     if (waves <= 0) return 0;
-    return go(k_gepi, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+    if (a->ksplit >= 8) return go(k_gepi<8>, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
+    return go(k_gepi<4>, blocks_for_waves(waves), (hipStream_t)stream, ev0, ev1, *a);
 }
 
 extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
