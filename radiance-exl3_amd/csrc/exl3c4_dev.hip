@@ -1340,10 +1340,12 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int gb = (int)blockIdx.x - (a.plan ? 1 : 0);
     const int nwg = (a.T + 3) / 4, per_xcd = (nwg + 7) / 8;
     const int wg = (gb & 7) * per_xcd + (gb >> 3);
-    const int i = wg * 4 + (int)(threadIdx.x >> 6);
+    // the row, its owner and its sorted_tok taken wave-uniform: the class descriptor and the row's entries are then
+    // scalar loads that go out together, not vector loads each waited for
+    const int i = __builtin_amdgcn_readfirstlane(wg * 4 + (int)(threadIdx.x >> 6));
     if (wg >= nwg || i >= a.T) return;
     const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
-    const int e = owner_wave(a.off, a.n_expert, i, lane);       // the plan (beside) writes row_info later
+    const int e = __builtin_amdgcn_readfirstlane(owner_wave(a.off, a.n_expert, i, lane));   // the plan writes row_info
     const int tok = a.sorted[i];
     if (e < 0) return;
     const Exl3c4DevClass& K = a.cls[class_of(a, e)];
