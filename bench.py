@@ -295,6 +295,47 @@ def valu_roofline(weights, seconds):
             "floor_us": round(instr / VALU_PEAK_GINSTR / 1e3, 2)}
 
 
+def measured_peaks(torch):
+    """What this box reaches on plain library work, timed with events on torch's stream: HBM read (a sum over 4 GiB of
+    f32: 4 GiB read a launch), HBM copy (4 GiB read + 4 GiB written a launch) and fp16 dense GEMM (hipBLASLt through
+    torch.matmul, 8192^3, f32 accumulation). The rooflines report their fractions against these beside the spec peaks."""
+    def best_ms(fn, reps=8):
+        fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        return min(ts)
+    n = 1 << 30
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    read_gbps = 4.0 * n / (best_ms(lambda: x.sum()) * 1e-3) / 1e9
+    y = torch.empty_like(x)
+    copy_gbps = 8.0 * n / (best_ms(lambda: y.copy_(x)) * 1e-3) / 1e9
+    del x, y
+    m = 8192
+    g = torch.Generator(device="cuda").manual_seed(1)
+    a = torch.randn(m, m, device="cuda", dtype=torch.float16, generator=g)
+    b = torch.randn(m, m, device="cuda", dtype=torch.float16, generator=g)
+    gemm_tflops = 2.0 * m ** 3 / (best_ms(lambda: torch.matmul(a, b), 6) * 1e-3) / 1e12
+    del a, b
+    torch.cuda.empty_cache()
+    return {"hbm_read_GBps": round(read_gbps, 1), "hbm_copy_GBps": round(copy_gbps, 1),
+            "fp16_gemm_TFLOPs": round(gemm_tflops, 1),
+            "how": "best of 8 event-timed launches: sum of 4 GiB f32; copy of 4 GiB; torch.matmul f16 8192^3"}
+
+
+def add_measured(roofline, peak):
+    """The roofline's fraction of what the box measured (peak_measured) beside its fraction of the spec peak."""
+    if roofline is not None and peak:
+        roofline["peak_measured"] = peak
+        roofline["frac_measured"] = round(roofline["achieved"] / peak, 4)
+
+
 # ------------------------------------------------------------------------------------------ configs[1]: one expert
 def run_single_expert(args, torch, exl3c4):
     """One SwiGLU expert (gate/up 2048 -> 2 x 512, down 512 -> 2048) at K 3, 4, 5 and m 1, 4, 16 tokens, top_k 1: one
@@ -374,7 +415,8 @@ def run_prefill_layer(args, torch, exl3c4):
         "packed_weight_GBps": round(live * EXPERT_BYTES / t / 1e9, 1),
         "roofline": {"bound": "mfma", "achieved": round(gu_flops / (np.mean(durs) * 1e-3) / 1e12, 1),
                      "peak": 2500.0, "unit": "TFLOP/s",
-                     "frac": round(gu_flops / (np.mean(durs) * 1e-3) / 2.5e15, 4), "traffic": None,
+                     "frac": round(gu_flops / (np.mean(durs) * 1e-3) / 2.5e15, 4),
+                     "traffic": read_traffic("k_gu_pf_prefill"),
                      "kernel": "k_gu_pf<4,mul1> (gate_up prefill GEMM)", "avg_us": round(float(np.mean(durs)) * 1e3, 1),
                      "flops_per_launch": gu_flops},
         "cpu_baseline": None,
@@ -458,6 +500,8 @@ def main():
     ap.add_argument("--stack-layers", type=int, default=48)
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="with the default decode layer: skip the prefill layer's figures")
+    ap.add_argument("--no-peaks", dest="peaks", action="store_false",
+                    help="skip the measured HBM and GEMM ceilings (peaks_measured, roofline frac_measured)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run 20 plain device-to-device copies of BYTES (the HBM-counter calibration) and exit")
     args = ap.parse_args()
@@ -480,6 +524,7 @@ def main():
     torch.cuda.set_device(0)
     run = {2: run_single_expert, 3: run_decode_layer, 4: run_prefill_layer, 5: run_stack}[args.config]
     out = run(args, torch, exl3c4)
+    peaks = measured_peaks(torch) if args.peaks else None
     if args.config == 3 and args.prefill:
         # the prefill layer measured in the same run, its figures beside the decode line's
         pf = run_prefill_layer(args, torch, exl3c4)
@@ -487,6 +532,14 @@ def main():
                           "max_rows_per_expert": pf["config"]["max_rows_per_expert"],
                           "us_per_layer": round(pf["ms_per_step"] * 1e3, 1), "tokens_per_s": pf["value"],
                           "TFLOPs": pf["TFLOPs"], "mfma_frac": pf["mfma_frac"], "roofline": pf["roofline"]}
+    if peaks:
+        out["peaks_measured"] = peaks
+        hbm = max(peaks["hbm_read_GBps"], peaks["hbm_copy_GBps"])
+        rf = out.get("roofline")
+        if rf is not None:
+            add_measured(rf, hbm if rf["unit"] == "GB/s" else peaks["fp16_gemm_TFLOPs"])
+        if "prefill" in out:
+            add_measured(out["prefill"]["roofline"], peaks["fp16_gemm_TFLOPs"])
     print(json.dumps(out), flush=True)
 
 
