@@ -427,9 +427,9 @@ def run_prefill_layer(args, torch, exl3c4):
 # ------------------------------------------------------------------------------------------ 48 layers
 def run_stack(args, torch, exl3c4):
     """48 decode layers, all resident, K of gate_up and of down cycling through {2, 3, 4, 6, 8} (gate_up at layer l
-    takes cycle[l % 5], down cycle[(l + 2) % 5]); a layer whose two K agree is one gate_up_down launch, else gate_up
-    (h_rot 1) then down (h_rot 1) through an h buffer. A step is 8 tokens through all the layers, each layer with its
-    own routing draw."""
+    takes cycle[l % 5], down cycle[(l + 2) % 5]); each layer is one gate_up_down launch with down's K given apart
+    (the op's dn_bits); with --stack-split, as the reference's single-K op must run it: gate_up (h_rot 1) then down
+    (h_rot 1) through an h buffer. A step is 8 tokens through all the layers, each layer with its own routing draw."""
     cyc = (2, 3, 4, 6, 8)
     n_layers = args.stack_layers
     g = torch.Generator(device="cuda")
@@ -453,10 +453,10 @@ def run_stack(args, torch, exl3c4):
         _, _, suh, suh1, svh, dsuh, dsvh = keep
         gcls = exl3c4.make_class(2 * W, H, codes=gu, suh=suh, suh1=suh1, svh=svh, dn_suh=dsuh)
         D = draws[l]
-        if kg == kd:
+        if kg == kd or not args.stack_split:
             dcls = exl3c4.make_class(H, W, codes=dn, svh=dsvh)
             ops = [exl3c4.make_op(exl3c4.GU_DN, kg, CB, [gcls], D["x"], D["sorted_tok"], D["off"], y, M, TOP_K,
-                                  dn=[dcls])]
+                                  dn=[dcls], dn_bits=0 if kg == kd else kd)]
         else:
             dcls = exl3c4.make_class(H, W, codes=dn, suh=dsuh, svh=dsvh)
             ops = [exl3c4.make_op(exl3c4.GATE_UP, kg, CB, [gcls], D["x"], D["sorted_tok"], D["off"], h, M, TOP_K,
@@ -476,7 +476,9 @@ def run_stack(args, torch, exl3c4):
     t = ms / steps * 1e-3
     out = common(args, ms, steps, M / t, "tokens/s",
                  f"configs[4]: {n_layers} routed MoE decode layers resident, gate_up / down K cycling "
-                 "{2,3,4,6,8} per projection, 8 tokens, per-layer softmax top-10 routing; one step = all layers",
+                 "{2,3,4,6,8} per projection, 8 tokens, per-layer softmax top-10 routing; one step = all layers; "
+                 + ("a layer = gate_up then down (two ops)" if args.stack_split else
+                    "a layer = one gate_up_down launch (down's K apart)"),
                  {"layers": n_layers, "resident_codes_GB": round(resident / 1e9, 2),
                   "step_packed_bytes": int(step_bytes)})
     out.update({"packed_weight_GBps": round(step_bytes / t / 1e9, 1),
@@ -498,6 +500,8 @@ def main():
                     help="BASELINE.json configs[n-1]: 2 one expert, 3 decode layer (default), 4 prefill layer, "
                          "5 48-layer decode stack")
     ap.add_argument("--stack-layers", type=int, default=48)
+    ap.add_argument("--stack-split", action="store_true",
+                    help="configs[4]: run each mixed-K layer as gate_up then down (two ops) instead of one launch")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="with the default decode layer: skip the prefill layer's figures")
     ap.add_argument("--no-peaks", dest="peaks", action="store_false",

@@ -102,6 +102,9 @@ typedef struct Exl3c4Op {
     const int32_t* expert_offset;             /* [n_expert + 1] */
     void*          y;
     int64_t        T, y_cols, y_pitch;        /* rows, width, pitch (elements) of the output */
+    int32_t        dn_bits;                   /* gate_up_down: down's K when it differs from gate_up's (bits);
+                                                 0 = bits. No counterpart in the reference's op, which takes one K:
+                                                 a layer of mixed K runs there as gate_up then down */
 } Exl3c4Op;
 
 /* Bytes of scratch a launch of this op needs, from its parameters only (M * top_k rows at the band top, the classes'

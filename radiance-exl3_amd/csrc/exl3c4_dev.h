@@ -78,7 +78,8 @@ typedef struct Exl3c4Launch {
     int32_t        x_pitch, y_pitch, part_pitch, dacc_pitch, hbuf_pitch, g_out_pitch;   /* elements */
     int32_t        x_dtype, x_rows, x_cols_max;
     int32_t        T, n_expert, top_k, n_class;
-    int32_t        bits, codebook;
+    int16_t        bits, dn_bits;  /* gate_up's (and down's alone) K; down's K inside gate_up_down */
+    int32_t        codebook;
     int32_t        h_rot;         /* gate_up: rotate h for down; down: the input is already rotated */
     int32_t        a_rot;         /* gate_up: the input is already rotated (sorted rows [T][2 C]) */
     int32_t        h_from_gu;     /* down: stage h from gate_up's partial sums (gate_up_down); k_rot: halves a row */

@@ -1104,8 +1104,8 @@ __device__ __forceinline__ void row_h(const Exl3c4Launch& a, int i, const GuRows
 // coherent accesses (part_ld / part_st), so the bits do not depend on where a workgroup lands. Built for 7 workgroups
 // a CU up to K = 6 (the register count it holds either way at K = 4; the schedule this target gives measured 0.5 us
 // faster); K = 7, 8 keep the looser target, under which they need no spill.
-template <int BITS, int CB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS <= 6 ? 7 : 5, 8))) void k_gd(
+template <int BITS, int CB, int BD = BITS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((BITS > BD ? BITS : BD) <= 6 ? 7 : 5, 8))) void k_gd(
     const Exl3c4Launch a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
@@ -1113,7 +1113,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS <= 6 ?
     const int ugu = a.n_grp << a.ksplit_log2;
     if (slot < rows * ugu) {
         const int i = xcd + 8 * (slot / ugu);
-        const GuRows g = gu_unit<BITS, CB, true>(a, i, slot % ugu, a.lds_pitch_gu, lds);
+        const GuRows g = gu_unit<BITS, CB, true>(a, i, slot % ugu, a.lds_pitch_gu, lds);   // gate_up at K = BITS
         if (g.nrows > 0) {
             __shared__ int last_s;
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");          // this thread's sums are stored
@@ -1127,7 +1127,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS <= 6 ?
         return;
     }
     const int d = slot - rows * ugu;
-    if (d < rows * a.nblk) dn_unit<BITS, CB, true>(a, d % a.nblk, xcd + 8 * (d / a.nblk), lds);
+    if (d < rows * a.nblk) dn_unit<BD, CB, true>(a, d % a.nblk, xcd + 8 * (d / a.nblk), lds);     // down at K = BD
     else if (a.g_out) gather_empty(a, 8 * (d - rows * a.nblk) + xcd);  // the grid's last slots of each XCD
 }
 
@@ -1870,14 +1870,43 @@ extern "C" int exl3c4_dev_gepi(const Exl3c4Launch* a, void* stream, void* ev0, v
 }
 
 extern "C" int exl3c4_dev_dn(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemmFn f = by_bits<DnK>(a->bits, a->codebook);
+    const GemmFn f = by_bits<DnK>(a->dn_gd ? a->dn_bits : a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->T <= 0) return 0;
     return go2(f, dim3((unsigned)a->nblk, (unsigned)a->T), (hipStream_t)stream, ev0, ev1, dn_lds_bytes(a), *a);
 }
 
+// gate_up_down's kernel for gate_up's K and down's: the same K for every codebook, a mixed pair for mul1 (2..8 each)
+template <int BG, int BD> GemmFn gd_mixed_bd() { return k_gd<BG, EXL3C4_CB_MUL1, BD>; }
+template <int BG> GemmFn gd_mixed(int bd) {
+    switch (bd) {
+    case 2: return gd_mixed_bd<BG, 2>();
+    case 3: return gd_mixed_bd<BG, 3>();
+    case 4: return gd_mixed_bd<BG, 4>();
+    case 5: return gd_mixed_bd<BG, 5>();
+    case 6: return gd_mixed_bd<BG, 6>();
+    case 7: return gd_mixed_bd<BG, 7>();
+    case 8: return gd_mixed_bd<BG, 8>();
+    default: return nullptr;
+    }
+}
+static GemmFn gd_kernel(int bg, int bd, int cb) {
+    if (bg == bd) return by_bits<GdK>(bg, cb);
+    if (cb != EXL3C4_CB_MUL1) return nullptr;
+    switch (bg) {
+    case 2: return gd_mixed<2>(bd);
+    case 3: return gd_mixed<3>(bd);
+    case 4: return gd_mixed<4>(bd);
+    case 5: return gd_mixed<5>(bd);
+    case 6: return gd_mixed<6>(bd);
+    case 7: return gd_mixed<7>(bd);
+    case 8: return gd_mixed<8>(bd);
+    default: return nullptr;
+    }
+}
+
 extern "C" int exl3c4_dev_gd(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemmFn f = by_bits<GdK>(a->bits, a->codebook);
+    const GemmFn f = gd_kernel(a->bits, a->dn_bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->T <= 0 || a->n_grp <= 0 || a->nblk <= 0) return 0;
     const uint32_t gu_lds = (uint32_t)(a->chunk_rows * a->lds_pitch_gu * 2), dn_lds = dn_lds_bytes(a);
@@ -1952,7 +1981,7 @@ extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
 }
 
 extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
-    const GemmFn f = by_bits<DnPfK>(a->bits, a->codebook);
+    const GemmFn f = by_bits<DnPfK>(a->dn_gd ? a->dn_bits : a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
     Exl3c4Launch g = *a;

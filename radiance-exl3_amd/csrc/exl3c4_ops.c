@@ -117,6 +117,11 @@ typedef struct Carve {
  *                  sync (gate_up_down as one kernel)]
  *   prefill path: [row_info | plan | rotated input | gate_up sums | h (gate_up_down) | down accumulations]
  * row_info: each row's owner (and, decode path, chunk rows), written by the first kernel for those after it. */
+/* gate_up_down's down K (the op's dn_bits, else its bits). A mixed pair runs as one kernel for the mul1 codebook (the
+ * instantiations k_gd carries); other codebooks take the three-kernel decode form, which every K has. */
+static int dn_bits_of(const Exl3c4Op* o) { return o->dn_bits ? o->dn_bits : o->bits; }
+static int gd_pair(const Exl3c4Op* o) { return dn_bits_of(o) == o->bits || o->codebook == EXL3C4_CB_MUL1; }
+
 static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     const int op = o->op;
     const int64_t rc = max_rows(o), xc = max_cols(o);
@@ -157,7 +162,7 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
         k->part_pitch = rc;
         off += ALIGN_UP(s * T * rc * 4, 256);
     }
-    k->gd1 = op == EXL3C4_GU_DN && !k->pf && T >= GD_FUSE_ROWS;
+    k->gd1 = op == EXL3C4_GU_DN && !k->pf && T >= GD_FUSE_ROWS && gd_pair(o);
     k->h_gepi = op == EXL3C4_GU_DN && !k->pf && !k->gd1 && T >= GEPI_ROWS;
     k->h = off;
     if ((k->pf || k->gd1 || k->h_gepi) && op == EXL3C4_GU_DN) {
@@ -217,6 +222,8 @@ static int check(const Exl3c4Op* o) {
     if ((o->h_rot != 0 && o->h_rot != 1) || (o->a_rot != 0 && o->a_rot != 1)) return EXL3C4_E_INVAL;
     if (op != EXL3C4_GATE_UP && o->a_rot) return EXL3C4_E_INVAL;
     if (o->bits < 2 || o->bits > 8) return EXL3C4_E_DTYPE;
+    if (o->dn_bits && (o->dn_bits < 2 || o->dn_bits > 8)) return EXL3C4_E_DTYPE;
+    if (o->dn_bits && o->dn_bits != o->bits && op != EXL3C4_GU_DN) return EXL3C4_E_INVAL;
     if (op != EXL3C4_PREP_GU && (o->codebook < EXL3C4_CB_3INST || o->codebook > EXL3C4_CB_MUL1)) return EXL3C4_E_DTYPE;
     if (o->M < 1 || o->n_expert < 1 || o->top_k < 1 || o->T < 0) return EXL3C4_E_SHAPE;
     if (o->n_expert > 65536) return EXL3C4_E_SHAPE;
@@ -233,7 +240,7 @@ static int check(const Exl3c4Op* o) {
             if (d->codes_stride && (d->codes_stride % 4 || (uintptr_t)d->codes % 4)) return EXL3C4_E_ALIGN;
             if (d->svh_stride & 1) return EXL3C4_E_ALIGN;
             /* down's [cols, rows / 2] weight: a stacked entry holds its record, svh [cols] */
-            if (d->codes_stride && d->codes_stride < exl3c4_record_bytes(d->rows, d->cols, o->bits))
+            if (d->codes_stride && d->codes_stride < exl3c4_record_bytes(d->rows, d->cols, dn_bits_of(o)))
                 return EXL3C4_E_STRIDE;
             if (d->svh_stride && d->svh_stride < 2 * (int64_t)d->rows) return EXL3C4_E_STRIDE;
             if (d->codes_stride > INT32_MAX || d->svh_stride > INT32_MAX) return EXL3C4_E_STRIDE;
@@ -362,7 +369,8 @@ static void base_args(const Exl3c4Op* o, const Carve* k, char* s, Exl3c4Launch* 
     a->n_expert = (int32_t)o->n_expert;
     a->top_k = (int32_t)o->top_k;
     a->n_class = o->n_class;
-    a->bits = o->bits;
+    a->bits = (int16_t)o->bits;
+    a->dn_bits = (int16_t)dn_bits_of(o);
     a->codebook = o->codebook;
     a->x = o->x;
     a->x_pitch = (int32_t)o->x_pitch;

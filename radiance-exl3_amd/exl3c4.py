@@ -43,7 +43,7 @@ class Op(C.Structure):
                 ("cls", Class * 4), ("dn", Class * 4),
                 ("x", _p), ("x_dtype", _i32), ("x_rows", _i64), ("x_cols", _i64), ("x_pitch", _i64),
                 ("sorted_tok", _p), ("expert_offset", _p),
-                ("y", _p), ("T", _i64), ("y_cols", _i64), ("y_pitch", _i64)]
+                ("y", _p), ("T", _i64), ("y_cols", _i64), ("y_pitch", _i64), ("dn_bits", _i32)]
 
 
 def lib():
@@ -289,9 +289,9 @@ def make_class(rows, cols, codes=None, suh=None, suh1=None, svh=None, dn_suh=Non
 
 
 def make_op(op, bits, cb, classes, x, sorted_tok, expert_offset, y, M, top_k, h_rot=0, a_rot=0, dn=None,
-            x_bf16=False, n_expert=None) -> Op:
+            x_bf16=False, n_expert=None, dn_bits=0) -> Op:
     o = Op()
-    o.op, o.bits, o.codebook = op, bits, CB.get(cb, cb)
+    o.op, o.bits, o.codebook, o.dn_bits = op, bits, CB.get(cb, cb), dn_bits
     o.n_class, o.h_rot, o.a_rot = len(classes), h_rot, a_rot
     o.M, o.top_k = M, top_k
     o.n_expert = expert_offset.numel() - 1 if n_expert is None else n_expert

@@ -386,10 +386,10 @@ class Dev:
     def gd_op(self, y, M=None):
         """gate_up_down's op over this case, writing y."""
         c = self.case
-        assert c.dn_bits == c.bits
         dn = [self.ex.make_class(d["rows"], d["cols"], codes=d["codes"], svh=d["svh"]) for d in self.tabs["dn"]]
         return self.ex.make_op(self.ex.GU_DN, c.bits, c.cb, self.cls("gu"), self.x, self.sorted_tok, self.off, y,
-                               c.n_tok if M is None else M, c.top_k, dn=dn, x_bf16=c.x_bf16, n_expert=c.n_expert)
+                               c.n_tok if M is None else M, c.top_k, dn=dn, x_bf16=c.x_bf16, n_expert=c.n_expert,
+                               dn_bits=0 if c.dn_bits == c.bits else c.dn_bits)
 
     def gate_up_down(self):
         """gate_up_down's output; self.status is then None (two kernels) or 0 (one kernel, which went well)."""

@@ -197,6 +197,29 @@ def test_mixed_k_layer_split_chain(torch_cuda, k_gu, k_dn):
     dev.check_tables()
 
 
+@pytest.mark.parametrize("k_gu,k_dn,cb,n_tok,top_k,n_expert,geom", [
+    (2, 4, "mul1", 8, 10, 64, (2048, 512)),      # 80 rows: gate_up_down's single kernel at the pair (2, 4)
+    (6, 3, "mul1", 8, 10, 64, (2048, 512)),
+    (8, 2, "mul1", 8, 10, 64, (2048, 512)),      # the K = 8 occupancy target with a K = 2 down
+    (4, 6, "mul1", 2, 10, 64, (2048, 512)),      # 20 rows: the three-kernel decode form, down at its own K
+    (3, 5, "mcg", 8, 10, 64, (2048, 512)),       # a codebook without a mixed single kernel: the three-kernel form
+    (5, 3, "mul1", 32, 4, 16, (512, 256)),       # 128 rows over 16 experts: the prefill GEMMs at their own K
+])
+def test_mixed_k_gate_up_down_in_one_launch(torch_cuda, k_gu, k_dn, cb, n_tok, top_k, n_expert, geom):
+    """gate_up_down with down's K apart from gate_up's (the op's dn_bits) gives the split chain's bits: gate_up
+    (h_rot 1) at K_g, then down (h_rot 1) at K_d; and the chain within the bar of the oracle's."""
+    case = Case(seed=20261040 + 10 * k_gu + k_dn + n_tok, n_tok=n_tok, top_k=top_k, n_expert=n_expert, geoms=[geom],
+                bits=k_gu, cb=cb, dn_bits=k_dn)
+    dev = Dev(case)
+    say(f"configs[4] mixed gate_up_down K_g={k_gu} K_d={k_dn} {cb} T={case.T}")
+    gd = dev.gate_up_down()
+    assert dev.status in (None, 0)
+    h1 = dev.gate_up(h_rot=1)
+    assert np.array_equal(dev.down(h1, h_rot=1), gd)
+    assert chain_ok("mixed gate_up_down", bf16(gd), bf16(case.oracle_down(case.oracle_gate_up(h_rot=1), h_rot=1)))
+    dev.check_tables()
+
+
 # ------------------------------------------------------------------------------------------ the reference's shapes
 def test_reference_geometry_tp1_2560_by_640(torch_cuda):
     check_all(Case(seed=5, n_tok=4, top_k=10, n_expert=16, geoms=[(2560, 640)], bits=4, cb="mul1"), "real tp1")
