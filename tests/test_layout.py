@@ -105,6 +105,30 @@ def test_refusals_are_decided_on_the_host_before_any_write():
     assert _launch_rc(o) == -1                                # gate_up_down's down geometry is [K, N / 2]
 
 
+def test_down_k_apart_is_checked_on_the_host():
+    """Exl3c4Op.dn_bits (gate_up_down's down K, 0 = bits): K outside 2..8 refused, another op given one refused, and
+    down's record stride held against down's own K."""
+    o = _op(op=exl3c4.GU_DN)
+    o.dn_bits = 9
+    assert _launch_rc(o) == -2                                # RAD_E_DTYPE
+    o.dn_bits = 1
+    assert _launch_rc(o) == -2
+    o = _op(op=exl3c4.GATE_UP)
+    o.dn_bits = 3
+    assert _launch_rc(o) == -12                               # RAD_E_INVAL: only gate_up_down has a down K
+    o = _op(op=exl3c4.GU_DN)
+    o.dn_bits = o.bits
+    assert _launch_rc(o) == -20                               # the same K spelt out: accepted up to the scratch
+    o = _op(op=exl3c4.GU_DN, bits=2)
+    o.dn_bits = 8
+    rb = exl3c4.lib().exl3c4_record_bytes
+    rb.restype, rb.argtypes = C.c_int64, [C.c_int64, C.c_int64, C.c_int32]
+    o.dn[0].codes_stride = rb(o.dn[0].rows, o.dn[0].cols, 2)
+    assert _launch_rc(o) == -4                                # RAD_E_STRIDE: a K = 2 entry cannot hold K = 8
+    o.dn[0].codes_stride = rb(o.dn[0].rows, o.dn[0].cols, 8)
+    assert _launch_rc(o) == -20
+
+
 def test_scratch_is_sized_from_the_parameters_alone():
     o = _op(M=8, top_k=10, E=64)
     n1 = exl3c4.scratch_bytes(o)
