@@ -467,10 +467,16 @@ def run_stack(args, torch, exl3c4):
     scratch = torch.empty(max(exl3c4.scratch_bytes(o) for ops, _ in layer_ops for o in ops), dtype=torch.uint8,
                           device="cuda")
 
+    # gate_up_down's counter block, zeroed once and left zeroed by every launch (exl3c4_launch_ctr: no fill dispatch a
+    # layer); the layers run in order on one stream, so they share it
+    ctr = torch.zeros(max([exl3c4.ctr_bytes(o) for ops, _ in layer_ops for o in ops if o.op == exl3c4.GU_DN] + [256]),
+                      dtype=torch.uint8, device="cuda")
+
     def step(i, st):
         for ops, _ in layer_ops:
             for o in ops:
-                check_rc(exl3c4, exl3c4.launch(o, scratch, st))
+                rc = exl3c4.launch_ctr(o, scratch, ctr, st) if o.op == exl3c4.GU_DN else exl3c4.launch(o, scratch, st)
+                check_rc(exl3c4, rc)
     steps = max(1, min(args.steps, 20))
     ms = timed_graph(torch, step, steps, min(args.warmup, 3))
     t = ms / steps * 1e-3
