@@ -15,10 +15,12 @@ replayed, so host launch cost does not pace the GPU. Inputs are resident before 
 
 Prints ONE JSON line. `value` is tokens/s of the layer; `roofline` is the dominant kernel's (gate_up_down's single
 kernel) achieved packed-weight bandwidth against the 8 TB/s HBM peak, its duration timed live by events the dispatch
-itself stamps; `roofline_valu` the same kernel against the VALU issue rate its trellis decode is bound by; `prefill`
-the prefill layer (configs[3]: 2048 tokens, Zipf routing) measured in the same run; `cpu_baseline` times the CPU
-oracle (this repository's C restatement of the reference's exl3ref) on the same workload, on one thread and on the
-box's cores.
+itself stamps, on its live experts' codes and scale planes; `roofline_valu` the same kernel against the VALU issue
+rate its trellis decode is bound by (its counted instructions); `prefill` the prefill layer (configs[3]: 2048 tokens,
+Zipf routing) and `stack` the 48-layer mixed-K decode stack (configs[4]), both measured in the same run;
+`peaks_measured` the box's own ceilings from this library's calibration kernels (libexl3c4_calib.so: HBM stream read,
+VALU issue rate and clock, f16 MFMA rate); `cpu_baseline` times the CPU oracle (this repository's C restatement of
+the reference's exl3ref) on the same workload, on one thread and on the box's cores, and configs[0]'s single linear.
 """
 from __future__ import annotations
 
@@ -94,43 +96,70 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_baseline(draw, max_experts, seed):
-    """The oracle's gate_up_down on the live experts of one routing draw -- or the first `max_experts` of them, the
-    time scaled to all -- with freshly drawn canonical planes of the same geometry: once on one thread, once on the
-    box's cores (the oracle spreads live experts over OpenMP threads; its outputs do not depend on the count)."""
+def _median_s(fn, runs=3):
+    """One untimed warm run, then the median of `runs` timed runs (seconds, CLOCK_MONOTONIC via perf_counter)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baseline(draw, max_experts, seed, one_thread_experts=12):
+    """The oracle's gate_up_down (this repository's C restatement of exl3ref, oracle/exl3_oracle.c) on the live experts
+    of one routing draw, with freshly drawn canonical planes of the same geometry: on the box's cores over every live
+    expert (OpenMP over experts; the outputs do not depend on the count), and on one thread over the first
+    `one_thread_experts` of them, its time scaled to the layer. Each figure is the median of 3 runs after one warm run.
+    Beside them, configs[0]: the CPU single linear (K_in 2048 -> N_out 512, K=4 mul1, one token), the oracle's down op
+    on one expert -- the input rotation, the W_hat decode, the ascending-k f32 GEMV, had128 x svh -- on one thread."""
     import exl3c4_synth as syn
     import oracle
     rng = np.random.default_rng(seed)
     off, st = draw["off_np"], draw["st_np"]
-    live = [e for e in range(E) if off[e + 1] > off[e]]
-    take = live[:max_experts]
-    # the sample: the routing restricted to the taken experts, renumbered 0..n-1 (the same rows, the same work)
-    keep_rows = np.concatenate([np.arange(off[e], off[e + 1]) for e in take])
-    sub_st = st[keep_rows].astype(np.int32)
-    sub_off = np.zeros(len(take) + 1, np.int32)
-    sub_off[1:] = np.cumsum([off[e + 1] - off[e] for e in take])
-    n = len(take)
-    gu = {"rows": 2 * W, "cols": H, "codes": syn.random_codes(rng, 2 * W, H, BITS, n),
-          "suh": syn.sign_scales(rng, H, 1.0, n), "suh1": syn.sign_scales(rng, H, 1.0, n),
-          "svh": syn.sign_scales(rng, 2 * W, 1 / np.sqrt(H), n), "dn_suh": syn.sign_scales(rng, W, 1.0, n)}
-    dn = {"rows": H, "cols": W, "codes": syn.random_codes(rng, H, W, BITS, n),
-          "suh": gu["dn_suh"], "svh": syn.sign_scales(rng, H, 1 / np.sqrt(W), n)}
+    live = [e for e in range(E) if off[e + 1] > off[e]][:max_experts]
+
+    def sample(take):
+        # the routing restricted to the taken experts, renumbered 0..n-1 (the same rows, the same work)
+        keep_rows = np.concatenate([np.arange(off[e], off[e + 1]) for e in take])
+        sub_st = st[keep_rows].astype(np.int32)
+        sub_off = np.zeros(len(take) + 1, np.int32)
+        sub_off[1:] = np.cumsum([off[e + 1] - off[e] for e in take])
+        n = len(take)
+        gu = {"rows": 2 * W, "cols": H, "codes": syn.random_codes(rng, 2 * W, H, BITS, n),
+              "suh": syn.sign_scales(rng, H, 1.0, n), "suh1": syn.sign_scales(rng, H, 1.0, n),
+              "svh": syn.sign_scales(rng, 2 * W, 1 / np.sqrt(H), n), "dn_suh": syn.sign_scales(rng, W, 1.0, n)}
+        dn = {"rows": H, "cols": W, "codes": syn.random_codes(rng, H, W, BITS, n),
+              "suh": gu["dn_suh"], "svh": syn.sign_scales(rng, H, 1 / np.sqrt(W), n)}
+        return gu, dn, sub_st, sub_off
     x = draw["x_np"].view(np.uint16)
     oracle.lib()
-    times = {}
-    for threads in (1, oracle.default_threads()):
-        oracle.set_threads(threads)
-        t0 = time.perf_counter()
-        oracle.run_gate_up_down([gu], [dn], BITS, CB, x, sub_st, sub_off, TOP_K)
-        times[threads] = time.perf_counter() - t0
-    cores = max(times)
-    scale = len(live) / n
-    return {"value": round(M / (times[cores] * scale), 3), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "value_1thread": round(M / (times[1] * scale), 3), "nproc": os.cpu_count(), "cpu_model": cpu_model(),
-            "sample": (f"{n} of the {len(live)} live experts of one decode layer step (8 tokens, top-10, K=4 mul1), "
-                       f"oracle/exl3_oracle.c gate_up_down: {times[1]:.2f} s on 1 thread, {times[cores]:.2f} s on "
-                       f"{cores} (OpenMP over experts)" + (f", scaled x{scale:.2f} to the whole layer" if n < len(live)
-                                                         else ""))}
+    cores = oracle.default_threads()
+    gu, dn, sub_st, sub_off = sample(live)
+    oracle.set_threads(cores)
+    t_all = _median_s(lambda: oracle.run_gate_up_down([gu], [dn], BITS, CB, x, sub_st, sub_off, TOP_K))
+    take1 = live[:one_thread_experts]
+    gu1, dn1, st1, off1 = sample(take1)
+    oracle.set_threads(1)
+    t_one = _median_s(lambda: oracle.run_gate_up_down([gu1], [dn1], BITS, CB, x, st1, off1, TOP_K))
+    scale1 = len(live) / len(take1)
+    # configs[0]: one linear [N_out 512, K_in 2048] at K=4 mul1, one token (sorted row 0 -> expert 0)
+    lin = {"rows": W, "cols": H, "codes": syn.random_codes(rng, W, H, BITS, 1),
+           "suh": syn.sign_scales(rng, H, 1.0, 1), "svh": syn.sign_scales(rng, W, 1 / np.sqrt(H), 1)}
+    x1 = syn.normal_f16(rng, (1, H)).view(np.uint16)
+    t_lin = _median_s(lambda: oracle.run_op(oracle.OP_DOWN, [lin], BITS, CB, x1, np.zeros(1, np.int32),
+                                            np.array([0, 1], np.int32), 1))
+    oracle.set_threads(cores)
+    return {"value": round(M / t_all, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "value_1thread": round(M / (t_one * scale1), 3), "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": (f"one decode layer step (8 tokens, top-10, K=4 mul1), oracle/exl3_oracle.c gate_up_down, "
+                       f"median of 3 after a warm run: all {len(live)} live experts on {cores} threads "
+                       f"({t_all:.2f} s); the first {len(take1)} on 1 thread ({t_one:.2f} s, scaled x{scale1:.2f})"),
+            "configs0_linear": {"ms": round(t_lin * 1e3, 2), "threads": 1,
+                                "what": "configs[0]: one EXL3 linear 2048 -> 512 at K=4 mul1, 1 token: input rotation, "
+                                        "W_hat decode of 1,048,576 weights, ascending-k f32 GEMV, had128 x svh "
+                                        "(the oracle's down op), median of 3 after a warm run"}}
 
 
 def read_traffic(name):
@@ -249,9 +278,12 @@ def run_decode_layer(args, torch, exl3c4):
     layer_gbps = float(np.mean(live)) * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
     one = T >= exl3c4.GD_FUSE_MIN_T           # gate_up_down runs as one kernel: that kernel is the one timed
     durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP_DOWN if one else exl3c4.K_GATE_UP, args.steps)
-    gemv_bytes = np.array(live, dtype=np.float64) * (CODE_BYTES if one else GU_CODE_BYTES)
+    # the kernel's algorithmic bytes: its live experts' packed codes and scale planes (perfmoe's definition)
+    gemv_bytes = np.array(live, dtype=np.float64) * (EXPERT_BYTES if one else GU_CODE_BYTES)
     gemv_gbps = float(np.mean(gemv_bytes) / (np.mean(durs) * 1e-3) / 1e9)
     kname = "k_gd_decode" if one else "k_gu_decode"
+    # the memory floor of the same bytes: the step's live experts' planes read the way the kernel reads them
+    floor = extent_read_floor(torch, layers, draws, n) if args.peaks else None
     cpu = cpu_baseline(draws[0], args.cpu_experts, args.seed + 2) if args.cpu_experts > 0 else None
     out = common(args, ms, args.steps, M * args.steps / (ms / 1e3), "tokens/s",
                  "configs[2]: routed MoE layer decode, 512 experts (gate/up 2048->2x512, down 512->2048) at 4 bpw "
@@ -269,36 +301,129 @@ def run_decode_layer(args, torch, exl3c4):
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(kname),
                      "kernel": "k_gd<4,mul1> (gate_up_down, one kernel)" if one else "k_gu<4,mul1> (gate_up GEMM)",
                      "avg_us": round(float(np.mean(durs)) * 1e3, 3),
-                     "bytes_per_launch": round(float(np.mean(gemv_bytes)))},
-        "roofline_valu": valu_roofline(float(np.mean(gemv_bytes)) * 8 / BITS, float(np.mean(durs)) * 1e-3),
+                     "bytes_per_launch": round(float(np.mean(gemv_bytes))),
+                     "bytes_what": "live experts x (packed codes + suh, suh1, svh, dn_suh, dn_svh): 1,588,224 B each"},
+        "roofline_valu": valu_roofline(float(np.mean(live)), float(np.mean(durs)) * 1e-3),
         "cpu_baseline": cpu,
     })
+    if floor:
+        out["roofline"]["extent_read_floor"] = floor
     return out
 
 
 # The decode loop's VALU work, read from the gfx950 assembly of k_gd<4,mul1> (the same loop body in k_gu / k_dn): an
 # iteration of two steps -- each step a wave's 32-column strip over 64 k, 2048 weights -- issues 253 VALU instructions
 # (64 v_pk_mul_lo_u16, 64 v_mad_u32_u16, 32 v_sad_u8, 32 v_sad_hi_u8, 32 v_pk_fma_f16, 18 v_alignbit_b32, 6 v_perm_b32,
-# 5 others) and 8 MFMAs.
+# 5 others) and 8 MFMAs. The kernel's whole issue (its start-ups, epilogues, gather) is counted by SQ_INSTS_VALU in
+# profiles/valu_k_gd_decode.json when that profile exists, and the line uses the count.
 VALU_PER_STEP, WEIGHTS_PER_STEP = 126.5, 2048
-# A SIMD issues one wave64 VALU instruction each 4 cycles (measured 1.8-1.95 ns each for the decode's instructions);
-# 1024 SIMDs at MI355X's 2.4 GHz peak engine clock.
+# A SIMD issues one wave64 VALU instruction each 4 cycles; 1024 SIMDs at MI355X's 2.4 GHz peak engine clock.
 VALU_PEAK_GINSTR = 1024 * 2.4 / 4
 
 
-def valu_roofline(weights, seconds):
-    """The decode kernel against the VALU issue roofline: its loop's wave instructions over the kernel's duration."""
-    instr = weights / WEIGHTS_PER_STEP * VALU_PER_STEP
+def read_counted_valu():
+    """SQ_INSTS_VALU a k_gd dispatch and the mean live experts of the run it was counted on (the committed rocprofv3
+    --pmc summary), or None."""
+    p = os.path.join(ROOT, "profiles", "valu_k_gd_decode.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
+
+
+def valu_roofline(live, seconds, peak_measured=None):
+    """The decode kernel against the VALU issue roofline: its wave instructions over its duration. The instructions
+    are the counted SQ_INSTS_VALU a dispatch (scaled to this run's live experts) when the profile is committed, else
+    the loop's count alone."""
+    c = read_counted_valu()
+    if c:
+        instr = float(c["sq_insts_valu_per_dispatch"]) * live / float(c["mean_live_experts"])
+        how = (f"SQ_INSTS_VALU a dispatch ({c['sq_insts_valu_per_dispatch']:.4g} at {c['mean_live_experts']} live "
+               f"experts, profiles/valu_k_gd_decode.json), scaled to this run's {live:.2f}")
+    else:
+        instr = live * 3 * W * H / WEIGHTS_PER_STEP * VALU_PER_STEP
+        how = "the decode loop's 126.5 instructions a 2048-weight step only (no counter profile committed)"
     achieved = instr / seconds / 1e9
-    return {"bound": "valu", "achieved": round(achieved, 1), "peak": VALU_PEAK_GINSTR, "unit": "G wave-instr/s",
-            "frac": round(achieved / VALU_PEAK_GINSTR, 4), "instr_per_launch": round(instr),
-            "floor_us": round(instr / VALU_PEAK_GINSTR / 1e3, 2)}
+    out = {"bound": "valu", "achieved": round(achieved, 1), "peak": VALU_PEAK_GINSTR, "unit": "G wave-instr/s",
+           "frac": round(achieved / VALU_PEAK_GINSTR, 4), "instr_per_launch": round(instr),
+           "floor_us": round(instr / VALU_PEAK_GINSTR / 1e3, 2), "instr_how": how}
+    if peak_measured:
+        out["peak_measured"] = peak_measured
+        out["frac_measured"] = round(achieved / peak_measured, 4)
+    return out
+
+
+_calib = None
+
+
+def calib():
+    """libexl3c4_calib.so: this library's own stream-read, VALU-issue and MFMA kernels (the box's ceilings)."""
+    global _calib
+    if _calib is None:
+        import ctypes as C
+        _calib = C.CDLL(os.path.join(ROOT, "radiance-exl3_amd", "libexl3c4_calib.so"))
+        f, p, i32, i64 = C.c_float, C.c_void_p, C.c_int32, C.c_int64
+        _calib.exl3c4_calib_read.restype = f
+        _calib.exl3c4_calib_read.argtypes = [p, i64, i32, p, i32, p]
+        _calib.exl3c4_calib_read_runs.restype = f
+        _calib.exl3c4_calib_read_runs.argtypes = [p, p, i32, i64, i32, p, i32, p]
+        _calib.exl3c4_calib_valu.restype = f
+        _calib.exl3c4_calib_valu.argtypes = [i32, i32, p, i32, p]
+        _calib.exl3c4_calib_mfma.restype = f
+        _calib.exl3c4_calib_mfma.argtypes = [i32, i32, p, i32, p]
+    return _calib
+
+
+def _ok_ms(ms, what):
+    if ms <= 0:
+        raise RuntimeError(f"{what}: calibration kernel failed ({ms})")
+    return ms
+
+
+def extent_read_floor(torch, layers, draws, n):
+    """The decode kernel's bytes as a plain read: for each step's layer and draw, every live expert's gate_up and down
+    codes read in 8 KiB runs (a wave a run, 1 KiB a step, two steps in flight: the decode kernels' access), all steps'
+    extents in one launch each; the rate over the codes (GB/s), best of 8."""
+    C = calib()
+    st = torch.cuda.current_stream().cuda_stream
+    sc = torch.zeros(64, dtype=torch.int32, device="cuda")
+    rates = []
+    for s in range(min(n, 8)):
+        L, D = layers[s % len(layers)], draws[s % len(draws)]
+        off = D["off_np"]
+        ext = []
+        for e in range(E):
+            if off[e + 1] > off[e]:
+                ext.append((L["gu_codes"][e].data_ptr(), L["gu_codes"][e].numel()))
+                ext.append((L["dn_codes"][e].data_ptr(), L["dn_codes"][e].numel()))
+        run = 8192
+        assert all(b % run == 0 for _, b in ext)
+        first = np.cumsum([0] + [b // run for _, b in ext[:-1]]).astype(np.int64)
+        n_runs = int(sum(b // run for _, b in ext))
+        ext_t = torch.from_numpy(np.array(ext, np.uint64).view(np.int64).reshape(-1)).cuda()
+        first_t = torch.from_numpy(first).cuda()
+        ms = _ok_ms(C.exl3c4_calib_read_runs(ext_t.data_ptr(), first_t.data_ptr(), len(ext), n_runs, run,
+                                             sc.data_ptr(), 8, st), "read_runs")
+        rates.append(sum(b for _, b in ext) / (ms * 1e-3) / 1e9)
+    return {"GBps": round(float(np.median(rates)), 1), "unit": "GB/s on the codes",
+            "how": "libexl3c4_calib.so k_read_runs: the step's live experts' codes in 8 KiB runs, a wave a run, "
+                   "1 KiB a step, two in flight; median over the draws of the best of 8"}
 
 
 def measured_peaks(torch):
-    """What this box reaches on plain library work, timed with events on torch's stream: HBM read (a sum over 4 GiB of
-    f32: 4 GiB read a launch), HBM copy (4 GiB read + 4 GiB written a launch) and fp16 dense GEMM (hipBLASLt through
-    torch.matmul, 8192^3, f32 accumulation). The rooflines report their fractions against these beside the spec peaks."""
+    """What this box reaches, on this library's own kernels (libexl3c4_calib.so, event-timed, best of 8): HBM read (a
+    4 GiB stream, 16-byte loads, four in flight a thread), the VALU issue rate of the trellis decode's own
+    instructions (8 independent chains a wave, 4 to 8 waves a SIMD) and with it the engine clock under that load, and
+    the f16 MFMA rate (v_mfma_f32_16x16x32_f16, 8 independent chains a wave); beside them torch's plain copy and
+    hipBLASLt's f16 GEMM (library work)."""
+    C = calib()
+    st = torch.cuda.current_stream().cuda_stream
+    n = 1 << 30
+    x = torch.ones(n, dtype=torch.float32, device="cuda")
+    sc = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    read = max(4.0 * n / (_ok_ms(C.exl3c4_calib_read(x.data_ptr(), 4 * n, blocks, sc.data_ptr(), 8, st),
+                                 "read") * 1e-3) / 1e9 for blocks in (2048, 4096, 8192))
+
     def best_ms(fn, reps=8):
         fn()
         torch.cuda.synchronize()
@@ -311,12 +436,21 @@ def measured_peaks(torch):
             b.synchronize()
             ts.append(a.elapsed_time(b))
         return min(ts)
-    n = 1 << 30
-    x = torch.ones(n, dtype=torch.float32, device="cuda")
-    read_gbps = 4.0 * n / (best_ms(lambda: x.sum()) * 1e-3) / 1e9
     y = torch.empty_like(x)
     copy_gbps = 8.0 * n / (best_ms(lambda: y.copy_(x)) * 1e-3) / 1e9
     del x, y
+    rounds = 2000
+    valu = []
+    for wg_per_cu in (4, 8):              # 4 or 8 waves a SIMD
+        blocks = 256 * wg_per_cu
+        ms = _ok_ms(C.exl3c4_calib_valu(blocks, rounds, sc.data_ptr(), 8, st), "valu")
+        valu.append(blocks * 4 * rounds * 56 / (ms * 1e-3) / 1e9)
+    valu_g = max(valu)
+    mfma = []
+    for wg_per_cu in (4, 8):
+        blocks = 256 * wg_per_cu
+        ms = _ok_ms(C.exl3c4_calib_mfma(blocks, rounds, sc.data_ptr(), 8, st), "mfma")
+        mfma.append(blocks * 4 * rounds * 8 * 16 * 16 * 32 * 2 / (ms * 1e-3) / 1e12)
     m = 8192
     g = torch.Generator(device="cuda").manual_seed(1)
     a = torch.randn(m, m, device="cuda", dtype=torch.float16, generator=g)
@@ -324,9 +458,13 @@ def measured_peaks(torch):
     gemm_tflops = 2.0 * m ** 3 / (best_ms(lambda: torch.matmul(a, b), 6) * 1e-3) / 1e12
     del a, b
     torch.cuda.empty_cache()
-    return {"hbm_read_GBps": round(read_gbps, 1), "hbm_copy_GBps": round(copy_gbps, 1),
-            "fp16_gemm_TFLOPs": round(gemm_tflops, 1),
-            "how": "best of 8 event-timed launches: sum of 4 GiB f32; copy of 4 GiB; torch.matmul f16 8192^3"}
+    return {"hbm_read_GBps": round(read, 1), "hbm_copy_GBps": round(copy_gbps, 1),
+            "valu_Ginstr_s": round(valu_g, 1), "valu_clock_GHz": round(valu_g * 4 / 1024, 3),
+            "mfma_f16_TFLOPs": round(max(mfma), 1), "fp16_gemm_TFLOPs": round(gemm_tflops, 1),
+            "how": ("best of 8 event-timed launches: libexl3c4_calib.so k_read over 4 GiB (hbm_read), k_valu (the "
+                    "mul1 pair's 7 instructions x 8 chains a wave; clock = rate x 4 cycles / 1024 SIMDs), k_mfma "
+                    "(v_mfma_f32_16x16x32_f16 x 8 chains a wave); torch copy_ of 4 GiB (read + write bytes); "
+                    "torch.matmul f16 8192^3 (hipBLASLt)")}
 
 
 def add_measured(roofline, peak):
@@ -510,6 +648,8 @@ def main():
                     help="configs[4]: run each mixed-K layer as gate_up then down (two ops) instead of one launch")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="with the default decode layer: skip the prefill layer's figures")
+    ap.add_argument("--no-stack", dest="stack", action="store_false",
+                    help="with the default decode layer: skip the 48-layer stack's figures")
     ap.add_argument("--no-peaks", dest="peaks", action="store_false",
                     help="skip the measured HBM and GEMM ceilings (peaks_measured, roofline frac_measured)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
@@ -537,19 +677,34 @@ def main():
     peaks = measured_peaks(torch) if args.peaks else None
     if args.config == 3 and args.prefill:
         # the prefill layer measured in the same run, its figures beside the decode line's
+        torch.cuda.empty_cache()
         pf = run_prefill_layer(args, torch, exl3c4)
         out["prefill"] = {"workload": pf["config"]["workload"], "rows": pf["config"]["rows"],
                           "max_rows_per_expert": pf["config"]["max_rows_per_expert"],
                           "us_per_layer": round(pf["ms_per_step"] * 1e3, 1), "tokens_per_s": pf["value"],
                           "TFLOPs": pf["TFLOPs"], "mfma_frac": pf["mfma_frac"], "roofline": pf["roofline"]}
+    if args.config == 3 and args.stack:
+        # the 48-layer stack measured in the same run
+        torch.cuda.empty_cache()
+        sk = run_stack(args, torch, exl3c4)
+        out["stack"] = {"workload": sk["config"]["workload"], "layers": sk["config"]["layers"],
+                        "resident_codes_GB": sk["config"]["resident_codes_GB"],
+                        "us_per_step": round(sk["ms_per_step"] * 1e3, 1), "tokens_per_s": sk["value"],
+                        "packed_weight_GBps": sk["packed_weight_GBps"], "hbm_frac": sk["hbm_frac"]}
+        torch.cuda.empty_cache()
     if peaks:
         out["peaks_measured"] = peaks
         hbm = max(peaks["hbm_read_GBps"], peaks["hbm_copy_GBps"])
+        mf = max(peaks["mfma_f16_TFLOPs"], peaks["fp16_gemm_TFLOPs"])
         rf = out.get("roofline")
         if rf is not None:
-            add_measured(rf, hbm if rf["unit"] == "GB/s" else peaks["fp16_gemm_TFLOPs"])
+            add_measured(rf, hbm if rf["unit"] == "GB/s" else mf)
+        rv = out.get("roofline_valu")
+        if rv is not None:
+            rv["peak_measured"] = peaks["valu_Ginstr_s"]
+            rv["frac_measured"] = round(rv["achieved"] / peaks["valu_Ginstr_s"], 4)
         if "prefill" in out:
-            add_measured(out["prefill"]["roofline"], peaks["fp16_gemm_TFLOPs"])
+            add_measured(out["prefill"]["roofline"], mf)
     print(json.dumps(out), flush=True)
 
 

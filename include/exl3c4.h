@@ -297,6 +297,18 @@ int     exl3c4_import_weight(Exl3c4Ckpt* ckpt, const char* name, int32_t bits, i
  *   exl3c4_plugin_inst_blocks_used   the blocks handed out so far */
 int32_t exl3c4_plugin_inst_flag(void* inst, int32_t block, int32_t set);
 int32_t exl3c4_plugin_inst_blocks_used(void* inst);
+/* The device address of an instance's counter block `block` (its status word first, then a counter a sorted row, 256
+ * bytes apart) and its size in bytes, or null past the blocks handed out: for a test that drives the kernel's own
+ * failure report from the host (a status word set before a launch, a counter no count can complete). */
+void*   exl3c4_plugin_inst_block(void* inst, int32_t block, int64_t* bytes);
+
+/* ------------------------------------------------------------------ the narrowing conversions (checkers' entries)
+ * The device's own f32 -> bf16 and f32 -> f16 conversions, as the kernels' outputs use them (down's y: one
+ * v_cvt_pk_bf16_f32 for two values; h: round to nearest even on an f32 value), over n f32 values: out[j] = the 16-bit
+ * result of in[j]. For a checker that holds them to the reference's rules (rad_f32_to_bf16: round to nearest even, a
+ * nan kept quiet as (u >> 16) | 0x40; rad_f32_to_f16: IEEE round to nearest even) over every input class. No
+ * counterpart in the reference. Returns 0 or EXL3C4_E_DEVICE; EXL3C4_E_SHAPE for n < 0 or n > 2^40. */
+int exl3c4_check_narrow(const float* in, uint16_t* out_bf16, uint16_t* out_f16, int64_t n, void* stream);
 
 /* Library identity: "gfx950" and the ABI version above. */
 const char* exl3c4_build_target(void);

@@ -45,6 +45,14 @@ uint16_t or_f32_to_bf16(float f) {
     return (uint16_t)(u >> 16);
 }
 
+/* or_f32_to_bf16 and or_f32_to_f16 over an array (a checker's vector form of the two above). */
+void or_narrow(const float* in, uint16_t* bf, uint16_t* h, int64_t n) {
+    for (int64_t j = 0; j < n; ++j) {
+        bf[j] = or_f32_to_bf16(in[j]);
+        h[j] = or_f32_to_f16(in[j]);
+    }
+}
+
 float or_bf16_to_f32(uint16_t b) {
     const uint32_t u = (uint32_t)b << 16;
     float f;

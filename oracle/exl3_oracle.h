@@ -34,6 +34,7 @@ uint16_t or_half_from_double(double x);
 uint16_t or_f32_to_f16(float f);
 uint16_t or_f32_to_bf16(float f);
 float    or_bf16_to_f32(uint16_t b);
+void     or_narrow(const float* in, uint16_t* bf16_out, uint16_t* f16_out, int64_t n);
 
 /* ---- codebook (common/exl3_decode.c:43-67) */
 uint16_t or_codebook_value(uint32_t state, int codebook);

@@ -50,6 +50,7 @@ def _declare(L):
     L.or_half_from_double.argtypes = [C.c_double]
     L.or_f32_to_bf16.restype = C.c_uint16
     L.or_f32_to_bf16.argtypes = [C.c_float]
+    L.or_narrow.argtypes = [_p, _p, _p, _i64]
     L.or_codebook_value.restype = C.c_uint16
     L.or_codebook_value.argtypes = [C.c_uint32, C.c_int]
     L.or_codebook_table.argtypes = [C.c_int, _p]
@@ -196,6 +197,15 @@ def record_to_codes(record: np.ndarray, rows: int, cols: int, bits: int) -> np.n
     if rc:
         raise ValueError(f"or_record_to_codes rc={rc}")
     return out
+
+
+def narrow(values: np.ndarray):
+    """or_f32_to_bf16 and or_f32_to_f16 of each float32 value (bits passed as they are, nans included): two uint16
+    arrays (bf16 bits, f16 bits)."""
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    bf, h = np.zeros(v.size, np.uint16), np.zeros(v.size, np.uint16)
+    lib().or_narrow(_ptr(v), _ptr(bf), _ptr(h), v.size)
+    return bf, h
 
 
 def had128(v: np.ndarray) -> np.ndarray:

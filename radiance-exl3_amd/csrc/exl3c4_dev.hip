@@ -758,20 +758,29 @@ __device__ __forceinline__ int32_t* row_counter(const Exl3c4Launch& a, int i) {
 // formed h). The wait gives up after EXL3C4_WAIT_TICKS of the 100 MHz clock, or soon after another workgroup gave up,
 // and sets bit 0 of the status word sync[0] -- and *fail, a flag the host can read without a synchronisation, when
 // the launch has one (the plugin rows' instances) -- the output is then void; the launch still ends.
+// A status word already set when the wait begins also gives up at once, before any counter is read: a block whose
+// earlier launch gave up may hold stale counts (a late gate_up count lands after the row's down units zeroed the
+// row's counters), so every later launch on it is void and reports it again -- in the same launch -- until the
+// caller zeroes the block.
 #define EXL3C4_WAIT_TICKS 50000000ull
 __device__ __forceinline__ void wait_gate_up(const Exl3c4Launch& a, int i) {
     if (threadIdx.x == 0) {
         const int want = (a.n_grp << a.ksplit_log2) + 1;
         const int32_t* cnt = row_counter(a, i);
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        for (unsigned n = 1; __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < want; ++n) {
+        // the status word and the first poll go out together: no round trip more on the wait's path
+        const int32_t st = __hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int32_t c = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool give_up = (st & 1) != 0;
+        for (unsigned n = 1; !give_up && c < want; ++n) {
             __builtin_amdgcn_s_sleep(8);
-            if ((n & 15) == 0 && ((__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1) ||
-                                  __builtin_amdgcn_s_memrealtime() - t0 > EXL3C4_WAIT_TICKS)) {
-                __hip_atomic_fetch_or(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (a.fail) __hip_atomic_store(a.fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                break;
-            }
+            give_up = (n & 15) == 0 && ((__hip_atomic_load(a.sync, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 1) ||
+                                        __builtin_amdgcn_s_memrealtime() - t0 > EXL3C4_WAIT_TICKS);
+            c = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (give_up) {
+            __hip_atomic_fetch_or(a.sync, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.fail) __hip_atomic_store(a.fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
     __syncthreads();
@@ -1998,5 +2007,28 @@ extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols
     if (waves <= 0) return 0;
     hipLaunchKernelGGL(f, dim3(blocks_for_waves(waves)), dim3(256), 0, (hipStream_t)stream, (const uint32_t*)record,
                        rows, cols, (uint16_t*)w_hat, w_pitch);
+    return launched();
+}
+
+// The kernels' own narrowing conversions over a list of f32 values (a checker's view): f2bf2 (down's y) on pairs, and
+// f2h (h) on each value.
+__global__ __launch_bounds__(256) void k_narrow(const float* in, uint16_t* ob, uint16_t* oh, int64_t n) {
+    const int64_t j = 2 * ((int64_t)blockIdx.x * 256 + threadIdx.x);
+    if (j >= n) return;
+    const float lo = in[j], hi = j + 1 < n ? in[j + 1] : 0.f;
+    const uint32_t b = f2bf2(lo, hi);
+    ob[j] = (uint16_t)b;
+    oh[j] = f2h(lo);
+    if (j + 1 < n) {
+        ob[j + 1] = (uint16_t)(b >> 16);
+        oh[j + 1] = f2h(hi);
+    }
+}
+
+extern "C" int exl3c4_check_narrow(const float* in, uint16_t* out_bf16, uint16_t* out_f16, int64_t n, void* stream) {
+    if (n < 0 || (n + 511) / 512 > 0x7FFFFFFF) return EXL3C4_E_SHAPE;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(k_narrow, dim3((unsigned)((n + 511) / 512)), dim3(256), 0, (hipStream_t)stream, in, out_bf16,
+                       out_f16, n);
     return launched();
 }

@@ -457,6 +457,18 @@ int32_t exl3c4_plugin_inst_flag(void* inst, int32_t block, int32_t set) {
     return v;
 }
 
+void* exl3c4_plugin_inst_block(void* inst, int32_t block, int64_t* bytes) {
+    Inst* q = (Inst*)inst;
+    if (bytes) *bytes = 0;
+    if (!q || block < 0) return NULL;
+    pthread_mutex_lock(&q->mu);
+    const int n = q->used;
+    pthread_mutex_unlock(&q->mu);
+    if (block >= n) return NULL;
+    if (bytes) *bytes = q->block_bytes;
+    return q->ctr + block * (q->block_bytes / 4);
+}
+
 int32_t exl3c4_plugin_inst_blocks_used(void* inst) {
     Inst* q = (Inst*)inst;
     if (!q) return -1;

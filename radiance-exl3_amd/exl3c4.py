@@ -108,6 +108,8 @@ def lib():
         L.exl3c4_import_parse_name.argtypes = [C.c_char_p, C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_i32)]
         L.exl3c4_import_weight.restype = C.c_int
         L.exl3c4_import_weight.argtypes = [_p, C.c_char_p, _i32, _i32, _i64, _i64, _p, _i64, _p, _p, _p]
+        L.exl3c4_check_narrow.restype = C.c_int
+        L.exl3c4_check_narrow.argtypes = [_p, _p, _p, _i64, _p]
         L.exl3c4_build_target.restype = C.c_char_p
         L.exl3c4_abi_version.restype = C.c_int
         _lib = L
@@ -272,6 +274,20 @@ def dequant(record, rows: int, cols: int, bits: int, cb, stream=None):
     if rc:
         raise RuntimeError(f"exl3c4_dequant: {STATUS.get(rc, rc)}")
     return out
+
+
+def check_narrow(values, stream=None):
+    """The device's own f32 -> bf16 and f32 -> f16 narrowing (the kernels' outputs' conversions) of a float32 device
+    tensor: two uint16 numpy arrays (bf16 bits, f16 bits). A checker's entry (exl3c4_check_narrow)."""
+    import torch
+    n = values.numel()
+    ob = torch.empty(n, dtype=torch.int16, device=values.device)
+    oh = torch.empty(n, dtype=torch.int16, device=values.device)
+    rc = lib().exl3c4_check_narrow(_ptr(values), _ptr(ob), _ptr(oh), n, _stream(stream))
+    if rc:
+        raise RuntimeError(f"exl3c4_check_narrow: {STATUS.get(rc, rc)}")
+    torch.cuda.synchronize()
+    return ob.cpu().numpy().view(np.uint16), oh.cpu().numpy().view(np.uint16)
 
 
 def make_class(rows, cols, codes=None, suh=None, suh1=None, svh=None, dn_suh=None) -> Class:

@@ -113,6 +113,8 @@ def bind(lib):
     lib.exl3c4_plugin_inst_flag.argtypes = [C.c_void_p, C.c_int32, C.c_int32]
     lib.exl3c4_plugin_inst_blocks_used.restype = C.c_int32
     lib.exl3c4_plugin_inst_blocks_used.argtypes = [C.c_void_p]
+    lib.exl3c4_plugin_inst_block.restype = C.c_void_p
+    lib.exl3c4_plugin_inst_block.argtypes = [C.c_void_p, C.c_int32, C.POINTER(C.c_int64)]
     lib.exl3c4_scratch_bytes_geom.restype = C.c_int64
     lib.exl3c4_scratch_bytes_geom.argtypes = [C.c_int32, C.c_int32, C.POINTER(C.c_int32), C.POINTER(C.c_int32),
                                               C.c_int64, C.c_int64, C.c_int64]

@@ -157,6 +157,36 @@ def test_prefill_layer_configs3_against_the_oracle(layer):
     dev.check_tables()
 
 
+def test_middle_band_m256_against_the_oracle(layer):
+    """The band between decode and prefill (the reference serves every M >= 17 with its prefill rows,
+    kernels/exl3r4d/rows.c:255-315): M = 256 tokens, softmax top-10 over the layer's 512 experts, 2560 sorted rows,
+    below the prefill path's threshold here, so gate_up_down runs as the decode path's single kernel with chunks of
+    up to 16 rows. gate_up_down == its pair, the chain against the oracle's, down on the device's own h within one
+    bf16 ulp, and gate_up's f32 sums of sampled rows within 2e-3 x RMS of the oracle's ascending sums."""
+    import exl3c4
+    case0, dev0 = layer
+    case = case0.rerouted(seed=20261019, n_tok=256, top_k=10)
+    assert case.T == 2560 and case.T < 8 * case.n_expert and case.T >= exl3c4.GD_FUSE_MIN_T
+    counts = np.diff(case.off)
+    say(f"middle band M=256: {int(np.count_nonzero(counts))} live experts, hottest {int(counts.max())} rows")
+    dev = Dev(case, share=dev0)
+    gd = dev.gate_up_down()
+    assert dev.status == 0                                       # the single kernel, and no wait gave up
+    h1 = dev.gate_up(h_rot=1)
+    assert np.array_equal(dev.down(h1, h_rot=1), gd)
+    assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
+    assert chain_ok("middle band y (the whole chain)", bf16(gd), bf16(case.oracle_gate_up_down()))
+    dev.gate_up(h_rot=0)
+    acc = dev.last_acc()
+    hot, rows = _sample_rows(case, n_hot=8, n_other=32, seed=3)
+    want = _gu_acc_rows(case, case.oracle_prep(prefill=0), rows)
+    err = rel_err(acc[rows, :want.shape[1]], want)
+    say(f"middle band: gate_up f32 sums of {len(rows)} rows: max-abs/RMS {err:.2e}")
+    assert err <= TOL
+    assert np.array_equal(dev.gate_up_down(), gd)
+    dev.check_tables()
+
+
 def test_prefill_multichunk_hot_experts_through_every_op(torch_cuda):
     """The prefill path at the layer's shapes against the oracle op by op: 256 tokens, Zipf top-10 over 32 experts
     (2560 rows, the hottest of several 64-row chunks)."""
@@ -201,6 +231,11 @@ def test_mixed_k_layer_split_chain(torch_cuda, k_gu, k_dn):
     (2, 4, "mul1", 8, 10, 64, (2048, 512)),      # 80 rows: gate_up_down's single kernel at the pair (2, 4)
     (6, 3, "mul1", 8, 10, 64, (2048, 512)),
     (8, 2, "mul1", 8, 10, 64, (2048, 512)),      # the K = 8 occupancy target with a K = 2 down
+    (3, 6, "mul1", 8, 10, 64, (2048, 512)),      # the four other pairs the 48-layer stack runs (bench.py run_stack:
+    (4, 8, "mul1", 8, 10, 64, (2048, 512)),      # gate_up cycling {2,3,4,6,8}, down two places on), each its own
+    (6, 2, "mul1", 8, 10, 64, (2048, 512)),      # instantiation of k_gd<K_g, mul1, K_d> with its own register
+    (8, 3, "mul1", 8, 10, 64, (2048, 512)),      # allocation
+    (2, 4, "mul1", 8, 10, 512, (2048, 512)),     # the stack's first pair over a full layer's 512 experts
     (4, 6, "mul1", 2, 10, 64, (2048, 512)),      # 20 rows: the three-kernel decode form, down at its own K
     (3, 5, "mcg", 8, 10, 64, (2048, 512)),       # a codebook without a mixed single kernel: the three-kernel form
     (5, 3, "mul1", 32, 4, 16, (512, 256)),       # 128 rows over 16 experts: the prefill GEMMs at their own K

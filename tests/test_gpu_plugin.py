@@ -243,3 +243,62 @@ def test_gate_up_down_row_instance_counter_pool(torch_cuda):
         dev.check_guards("instance launches")
     finally:
         row.fini(inst)
+
+
+def test_gate_up_down_row_instance_kernel_reports_a_wait_that_gave_up(torch_cuda):
+    """The kernel's own failure report, driven from the host without any wait that must time out: before a launch on
+    a row instance's block, the host sets the block's status word and drives one live row's counter far negative (no
+    count can complete it). The single kernel's waits then give up at their first check (a status word already set
+    poisons the block), every kernel exits, and the kernel itself sets the status word and the instance's pinned
+    flag (kernels/exl3r4d/exl3r4d.hip:1878-1880 raises the reference's). The block's next launch returns RAD_E_DEVICE
+    and writes nothing; the one after it gives the good bits."""
+    import exl3c4
+    case = Case(seed=41, n_tok=8, top_k=10, n_expert=40, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
+    assert case.T >= exl3c4.GD_FUSE_MIN_T
+    dev = Dev(case)
+    p = Plug(dev)
+    want = dev.gate_up_down()
+    hip = exl3c4.hip()
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    hip.hipMemcpy.restype = C.c_int
+    row, inst = _gd_inst(p, 3)
+    try:
+        H = dev.tabs["gu"][0]["cols"]
+        y = dev.out(H)
+        assert p.run(3, dev.x, y, rp.BF16, inst=inst) == 0        # block 0: (this stream, y)
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+        nbytes = C.c_int64()
+        blk = p.lib.exl3c4_plugin_inst_block(inst, 0, C.byref(nbytes))
+        assert blk and nbytes.value > 0
+
+        def read_block():
+            h = np.zeros(nbytes.value // 4, np.int32)
+            assert hip.hipMemcpy(h.ctypes.data, blk, nbytes.value, 2) == 0    # device to host
+            return h
+
+        def write_word(index, value):
+            v = np.array([value], np.int32)
+            assert hip.hipMemcpy(blk + 4 * index, v.ctypes.data, 4, 1) == 0   # host to device
+
+        assert not read_block().any()                                # the good launch left its block zero
+        live = [i for i in range(case.T) if case.off[0] <= i < case.off[-1] and case.sorted_tok[i] >= 0]
+        i = live[len(live) // 2]
+        print(f"instance: status word set, row {i}'s counter driven negative, then a launch", flush=True)
+        write_word(0, 1)
+        write_word((i + 1) * 64, -(1 << 30))
+        y.fill_(0x2222)
+        assert p.run(3, dev.x, y, rp.BF16, inst=inst) == 0            # the launch itself goes out
+        assert read_block()[0] & 1                                   # ... its waits gave up: the status word
+        assert p.lib.exl3c4_plugin_inst_flag(inst, 0, -1) == 1       # ... and the kernel's write of the pinned flag
+        print("instance: the next launch reports it", flush=True)
+        y.fill_(0x1111)
+        assert p.run(3, dev.x, y, rp.BF16, inst=inst) == -21          # RAD_E_DEVICE, nothing written
+        assert (y.cpu().numpy() == 0x1111).all()
+        assert p.lib.exl3c4_plugin_inst_flag(inst, 0, -1) == 0
+        assert not read_block().any()                                # the report zeroed the block
+        assert p.run(3, dev.x, y, rp.BF16, inst=inst) == 0
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), want)
+        assert not read_block().any()
+        dev.check_guards("instance failure report")
+    finally:
+        row.fini(inst)

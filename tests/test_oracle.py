@@ -152,6 +152,50 @@ def test_fp16_round_trips_every_finite_half_and_rounds_ties_to_even(oracle_lib):
     assert all(f(x) == int(np.float16(x).view(np.uint16)) for x in xs)
 
 
+def _bf16_nearest(bits):
+    """bf16 round-to-nearest-even by distance (not by the bit trick): the two bf16 neighbours of each finite f32 as
+    float64, the nearer one, ties to the even mantissa; a value past the largest finite bf16's rounding boundary
+    becomes inf (IEEE)."""
+    b = np.asarray(bits, np.uint32)
+    x = b.view(np.float32).astype(np.float64)
+    lo = (b >> 16).astype(np.uint32)
+    sign = lo & 0x8000
+    mag = lo & 0x7FFF
+    down = ((sign | mag) << 16).view(np.float32).astype(np.float64)
+    up_bits = (sign | (mag + 1)) & 0xFFFF
+    up = (up_bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    up = np.where((up_bits & 0x7FFF) == 0x7F80, np.where(sign != 0, -2.0 ** 128, 2.0 ** 128), up)   # inf's place
+    dd, du = np.abs(x - down), np.abs(up - x)
+    pick_up = (du < dd) | ((du == dd) & ((mag & 1) == 1))
+    return np.where(pick_up, up_bits, sign | mag).astype(np.uint16)
+
+
+def test_bf16_narrowing_is_round_to_nearest_even_with_quiet_nans(oracle_lib):
+    """or_f32_to_bf16 (radiance's rad_f32_to_bf16) against the nearest bf16 by distance, over every upper half-word
+    with the low halves 0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF and random patterns; nans stay nans, quiet, with their
+    upper payload; or_f32_to_f16 against numpy's float32 -> float16 (IEEE round to nearest even)."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    rng = np.random.default_rng(11)
+    bits = np.concatenate([(hi[:, None] | lows[None, :]).ravel(),
+                           rng.integers(0, 1 << 32, size=200000, dtype=np.uint64).astype(np.uint32)])
+    bf, h = oracle.narrow(bits.view(np.float32))
+    nan = (bits & 0x7FFFFFFF) > 0x7F800000
+    fin = (bits & 0x7F800000) != 0x7F800000
+    assert np.array_equal(bf[fin], _bf16_nearest(bits[fin]))
+    assert np.array_equal(bf[nan], ((bits[nan] >> 16) | 0x40).astype(np.uint16))
+    inf = ~nan & ~fin
+    assert np.array_equal(bf[inf], (bits[inf] >> 16).astype(np.uint16))
+    with np.errstate(over="ignore"):
+        want_h = bits[~nan].view(np.float32).astype(np.float16).view(np.uint16)
+    assert np.array_equal(h[~nan], want_h)
+    # spot values: a tie rounds to even (down, then up), past the largest finite goes to inf
+    t = lambda u: int(oracle.narrow(np.array([u], np.uint32).view(np.float32))[0][0])  # noqa: E731
+    assert t(0x3F808000) == 0x3F80 and t(0x3F818000) == 0x3F82 and t(0x7F7F8000) == 0x7F80
+    # negative control: truncation is not the rule
+    assert not np.array_equal(bf[fin], (bits[fin] >> 16).astype(np.uint16))
+
+
 def test_had128_is_the_normalised_sylvester_hadamard(oracle_lib):
     v = np.zeros(256, np.float32)
     v[0] = 1
