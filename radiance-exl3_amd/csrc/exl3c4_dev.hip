@@ -603,25 +603,25 @@ __device__ __forceinline__ void gemv_strip(gu32p rec, int ksn, CodeRing<BITS>& r
 
 // gate_up's staging of a split's input rows in LDS (the split's 128-blocks [b0, b1)): as given (AROT: x holds the
 // rotated rows, the gate half then the up half) or f16(had128(f16(x * s))) of the row's token (s = suh or suh1, zero
-// for a negative sorted_tok). The (row, block) pairs of the chunk, row-major, are dealt to the four waves, GU_PB a wave
+// for a negative sorted_tok). The (row, block) pairs of the chunk, row-major, are dealt to the four waves, PB a wave
 // a round: a round's input and scale loads all go out before any is used, none behind a branch (a pair past the last
 // loads the last, unused), so a round costs one memory round trip however its pairs fall over rows and blocks (a chunk
 // of 16 rows and one block: one round, not 16 round trips in series). The codes' first steps go out right after the
 // first round's inputs, so they are in flight while it is staged; the codes are not waited for before the loop.
-template <int BITS, bool AROT>
-__device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows, int KC, bool up, int b0, int b1,
-                                         int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
-                                         uint16_t* A, int kp) {
+// A chunk of at most four pairs (the decode layer's one-row chunks: a split's four blocks) takes one round of one pair
+// a wave, without the loads and addresses of three unused pairs a wave.
+template <int BITS, bool AROT, int PB>
+__device__ __forceinline__ void gu_stage_rounds(const Exl3c4Launch& a, int i, int npair, int nbs, int KC, bool up,
+                                                int b0, int tok_l, const void* sv, gu32p rec, int ksn,
+                                                CodeRing<BITS>& ring, uint16_t* A, int kp) {
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6), lane = threadIdx.x & 63, el = had_col(lane);
     const int eo = AROT ? el : had_col_t(lane);                   // where a staged value goes
-    constexpr int GU_PB = 4;
-    const int nbs = b1 - b0, npair = nrows * nbs;
     const bool bf = a.x_dtype == EXL3C4_BF16;
-    for (int p0 = 0; p0 < npair; p0 += 4 * GU_PB) {
-        int q[GU_PB], hb[GU_PB], tok[GU_PB];
-        uint16_t x0[GU_PB], x1[GU_PB], s0[GU_PB], s1[GU_PB];
+    for (int p0 = 0; p0 < npair; p0 += 4 * PB) {
+        int q[PB], hb[PB], tok[PB];
+        uint16_t x0[PB], x1[PB], s0[PB], s1[PB];
 #pragma unroll
-        for (int j = 0; j < GU_PB; ++j) {                         // wave-uniform: the pair's row and block
+        for (int j = 0; j < PB; ++j) {                            // wave-uniform: the pair's row and block
             const int pc = min(p0 + wave + 4 * j, npair - 1);
             q[j] = pc / nbs;
             hb[j] = b0 + (pc - q[j] * nbs);
@@ -634,12 +634,12 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
         }
         if (p0 == 0) prime<BITS>(rec, ksn, ring);
 #pragma unroll
-        for (int j = 0; j < GU_PB; ++j) {
+        for (int j = 0; j < PB; ++j) {
             s0[j] = AROT ? 0 : ldg16(sv, hb[j] * 128 + el);
             s1[j] = AROT ? 0 : ldg16(sv, hb[j] * 128 + 64 + el);
         }
 #pragma unroll
-        for (int j = 0; j < GU_PB; ++j) {
+        for (int j = 0; j < PB; ++j) {
             if (p0 + wave + 4 * j >= npair) break;                // uniform: the rotation's DPP runs the whole wave
             uint16_t v0 = x0[j], v1 = x1[j];
             if (!AROT) {
@@ -651,6 +651,14 @@ __device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows
             lds_put(A, q[j], kp, (hb[j] - b0) * 128, eo, v0, v1);
         }
     }
+}
+template <int BITS, bool AROT>
+__device__ __forceinline__ void gu_stage(const Exl3c4Launch& a, int i, int nrows, int KC, bool up, int b0, int b1,
+                                         int tok_l, const void* sv, gu32p rec, int ksn, CodeRing<BITS>& ring,
+                                         uint16_t* A, int kp) {
+    const int nbs = b1 - b0, npair = nrows * nbs;
+    if (npair <= 4) gu_stage_rounds<BITS, AROT, 1>(a, i, npair, nbs, KC, up, b0, tok_l, sv, rec, ksn, ring, A, kp);
+    else gu_stage_rounds<BITS, AROT, 4>(a, i, npair, nbs, KC, up, b0, tok_l, sv, rec, ksn, ring, A, kp);
 }
 
 // gate_up's GEMM: one workgroup per (sorted row i, group of four 32-column strips, k split). The workgroup keyed on
@@ -900,6 +908,25 @@ __device__ __forceinline__ DnW dn_weight(bool gd, const Exl3c4DevClass& K) {
     return DnW{ K.codes, K.svh, K.suh, K.codes_s, K.svh_s, K.suh_s, K.rows, K.cols };
 }
 
+// Down's staging of h inside gate_up_down's single launch: wave w stages h's block w of the chunk's rows (at most R),
+// every row's loads first, none behind a branch (rows past the chunk's last and blocks past h's last load those,
+// unused); R the least of 1, 4, 8, 16 that holds the chunk, so a one-row chunk issues two loads a lane, not 32.
+template <int R>
+__device__ __forceinline__ void dn_stage_h(const Exl3c4Launch& a, int i, int nrows, int nhb, int wave, int lane,
+                                           uint16_t* A, int kp) {
+    const int hb = wave;
+    uint16_t h0[R], h1[R];
+#pragma unroll
+    for (int q = 0; q < R; ++q) {
+        const uint16_t* hs = a.hbuf + (int64_t)(i + min(q, nrows - 1)) * a.hbuf_pitch + min(hb, nhb - 1) * 128;
+        h0[q] = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        h1[q] = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int q = 0; q < R; ++q)
+        if (q < nrows && hb < nhb) lds_put(A, q, kp, hb * 128, lane, h0[q], h1[q]);
+}
+
 template <int BITS, int CB, bool FUSED>
 __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, unsigned char* lds) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -948,22 +975,22 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
     const uint16_t sv0 = ldg16(svh, b * 128 + et), sv1 = ldg16(svh, b * 128 + 64 + et);
     const void* suh = (!a.h_from_gu && !a.h_rot) ? tab_entry(D.suh, D.suh_s, jx) : nullptr;
     if (FUSED) wait_gate_up(a, i);
+    // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the row's
+    // counters at its end, so a launch leaves them as it found them (the reference's counter blocks,
+    // kernels/exl3r4d/launch.c:311-324). Counted right after the wait, so the count's round trip runs under the
+    // staging and the loop rather than at the unit's end.
+    int done_old = 0;
+    if (FUSED && threadIdx.x == 0)
+        done_old = __hip_atomic_fetch_add(row_counter(a, i) + EXL3C4_SYNC_DONE, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
 
     // stage the chunk's rows
     const int nhb = KC / 128;
-    if (FUSED && nhb <= 4) {                                      // each wave one block of h: every row's loads first,
-        constexpr int R = EXL3C4_CHUNK_ROWS;                      // none behind a branch (rows past the chunk's last
-        const int hb = wave;                                      // and blocks past h's last load those, unused)
-        uint16_t h0[R], h1[R];
-#pragma unroll
-        for (int q = 0; q < R; ++q) {
-            const uint16_t* hs = a.hbuf + (int64_t)(i + min(q, nrows - 1)) * a.hbuf_pitch + min(hb, nhb - 1) * 128;
-            h0[q] = __hip_atomic_load(hs + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            h1[q] = __hip_atomic_load(hs + lane + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-        for (int q = 0; q < R; ++q)
-            if (q < nrows && hb < nhb) lds_put(A, q, kp, hb * 128, lane, h0[q], h1[q]);
+    if (FUSED && nhb <= 4) {                                      // each wave one block of h (dn_stage_h)
+        if (nrows <= 1) dn_stage_h<1>(a, i, nrows, nhb, wave, lane, A, kp);
+        else if (nrows <= 4) dn_stage_h<4>(a, i, nrows, nhb, wave, lane, A, kp);
+        else if (nrows <= 8) dn_stage_h<8>(a, i, nrows, nhb, wave, lane, A, kp);
+        else dn_stage_h<EXL3C4_CHUNK_ROWS>(a, i, nrows, nhb, wave, lane, A, kp);
     } else if (!FUSED && !a.h_from_gu) {                          // down's input rows (its op's, or h from k_gepi):
         // each of a wave's blocks with every row's loads first, none behind a branch (rows past the chunk load its
         // last, unused): a block costs one round trip, not one a row
@@ -1064,12 +1091,7 @@ __device__ __forceinline__ void dn_unit(const Exl3c4Launch& a, int b, int i, uns
         put_y(a, out, et, (uint16_t)yb, (uint16_t)(yb >> 16));
     }
     if (FUSED && a.g_out) gather_count(a, i, nrows, b, tok_l);
-    // every down unit of the row has passed its wait once the row's last one counts here: that one zeroes the row's
-    // counters, so a launch leaves them as it found them (the reference's counter blocks,
-    // kernels/exl3r4d/launch.c:311-324). Counted at the unit's end, so that the count's round trip delays no load.
-    if (FUSED && threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(row_counter(a, i) + EXL3C4_SYNC_DONE, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            N / 128 - 1) {
+    if (FUSED && threadIdx.x == 0 && done_old == N / 128 - 1) {
         __hip_atomic_store(row_counter(a, i), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(row_counter(a, i) + EXL3C4_SYNC_DONE, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
