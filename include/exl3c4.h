@@ -172,6 +172,12 @@ int     exl3c4_launch_noalloc(const Exl3c4Op* op, void* stream);
 enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3, EXL3C4_K_GATE_UP_DOWN = 4 };
 #define EXL3C4_GD_FUSE_MIN_T 32
 
+/* The least sorted-row count T at which gate_up, down and gate_up_down over n_expert experts take the prefill path (a chunk plan and one GEMM kernel a projection, decoding each weight once a chunk of up to 96
+ * rows of one expert) rather than the decode kernels: max(64, ceil(3 n_expert / 4)) -- the crossover measured on
+ * MI355X at the decode layer's experts. A function of T and n_expert only, never of the routing. A query with no
+ * counterpart in the reference (whose rows split the band at M = 17, kernels/exl3r4d/rows.c:255-315). */
+int64_t exl3c4_prefill_min_rows(int64_t n_expert);
+
 /* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and
  * ev_stop (two hipEvent_t the caller created) at its start and end: the duration of that one kernel, read with
  * hipEventElapsedTime, however the host paces the launches. A measurement entry with no counterpart in the reference
@@ -180,7 +186,7 @@ enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DO
 int exl3c4_launch_timed(const Exl3c4Op* op, void* scratch, int64_t scratch_bytes, void* stream, int32_t kernel,
                         void* ev_start, void* ev_stop);
 
-/* exl3c4_launch, and on the prefill path (a chunk plan: from 64 and 8 n_expert sorted rows) its GEMMs also write
+/* exl3c4_launch, and on the prefill path (a chunk plan: from exl3c4_prefill_min_rows sorted rows) its GEMMs also write
  * their f32 accumulations to scratch for exl3c4_scratch_partials -- 4 bytes a row and output column each, which the
  * production launch does not spend. The outputs are exl3c4_launch's, bit for bit. A checker's entry; no counterpart
  * in the reference. */

@@ -79,14 +79,24 @@ static int log2i(int v) {
     return l;
 }
 
-/* The prefill path serves a launch of at least 64 rows whose rows average at least this many an expert
- * (T >= n * n_expert): chunks of up to 64 rows share each decoded weight, over seven launches. Below it the decode
- * kernels (16-row chunks, split-K, two launches) serve it. A function of T and n_expert only (never of the routing). */
-#ifndef EXL3C4_PF_ROWS_PER_EXPERT
-#define EXL3C4_PF_ROWS_PER_EXPERT 8
+/* The prefill path (the rotation with the chunk plan, then one GEMM kernel a projection over chunks of up to 96 rows of
+ * one expert) serves a launch of at least 64 sorted rows that average at least 3/4 of a row an expert: T >= 64 and
+ * 4 T >= 3 n_expert (exl3c4_prefill_min_rows). Below it the decode kernels serve it (chunks of up to 16 rows, split-K;
+ * gate_up_down as one kernel from EXL3C4_GD_FUSE_MIN_T rows). The rule is the crossover measured on MI355X at the
+ * decode layer's experts (512 experts, 2048 / 512, K = 4, softmax top-10): gate_up_down by the decode kernels against
+ * the prefill kernels, us a launch, M tokens: M = 17: 99 / 110, 24: 118 / 128, 32: 148 / 149, 48: 187 / 184,
+ * 64: 219 / 210, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293. The reference serves M >= 17 by its GEMM rows
+ * (kernels/exl3r4d/rows.c:255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the band below the
+ * crossover. A function of T and n_expert only (never of the routing). */
+#ifndef EXL3C4_PF_MIN_T
+#define EXL3C4_PF_MIN_T 64
 #endif
+int64_t exl3c4_prefill_min_rows(int64_t n_expert) {
+    const int64_t r = (3 * (n_expert > 0 ? n_expert : 0) + 3) / 4;
+    return r > EXL3C4_PF_MIN_T ? r : EXL3C4_PF_MIN_T;
+}
 static int prefill_path(const Exl3c4Op* o, int64_t T) {
-    return o->op != EXL3C4_PREP_GU && T >= 64 && T >= EXL3C4_PF_ROWS_PER_EXPERT * o->n_expert;
+    return o->op != EXL3C4_PREP_GU && T >= exl3c4_prefill_min_rows(o->n_expert);
 }
 
 /* gate_up_down runs as one kernel at decode from this many sorted rows (the header's EXL3C4_GD_FUSE_MIN_T; a build
@@ -514,7 +524,7 @@ static int runs_kernel(const Exl3c4Op* o, const Carve* k, int kernel) {
     }
 }
 
-/* The launches of each op on the stream. Decode (fewer than 64 and 8 n_expert sorted rows: prefill_path) has no
+/* The launches of each op on the stream. Decode (fewer sorted rows than exl3c4_prefill_min_rows: prefill_path) has no
  * planning pass: every workgroup finds its rows' expert itself.
  *   prep_gu       the input rotation
  *   gate_up       its GEMM (input rotation staged inside), then its epilogue

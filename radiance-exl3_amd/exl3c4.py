@@ -108,6 +108,8 @@ def lib():
         L.exl3c4_import_parse_name.argtypes = [C.c_char_p, C.POINTER(_i32), C.POINTER(_i64), C.POINTER(_i32)]
         L.exl3c4_import_weight.restype = C.c_int
         L.exl3c4_import_weight.argtypes = [_p, C.c_char_p, _i32, _i32, _i64, _i64, _p, _i64, _p, _p, _p]
+        L.exl3c4_prefill_min_rows.restype = _i64
+        L.exl3c4_prefill_min_rows.argtypes = [_i64]
         L.exl3c4_check_narrow.restype = C.c_int
         L.exl3c4_check_narrow.argtypes = [_p, _p, _p, _i64, _p]
         L.exl3c4_build_target.restype = C.c_char_p
@@ -274,6 +276,15 @@ def dequant(record, rows: int, cols: int, bits: int, cb, stream=None):
     if rc:
         raise RuntimeError(f"exl3c4_dequant: {STATUS.get(rc, rc)}")
     return out
+
+
+def prefill_min_rows(n_expert: int) -> int:
+    """The least sorted-row count at which an op over n_expert experts takes the prefill path (exl3c4_prefill_min_rows)."""
+    return int(lib().exl3c4_prefill_min_rows(n_expert))
+
+
+def is_prefill(T: int, n_expert: int) -> bool:
+    return T >= prefill_min_rows(n_expert)
 
 
 def check_narrow(values, stream=None):

@@ -55,10 +55,11 @@ def _check(case, dev, y, acc, label):
 
 @pytest.mark.parametrize("bits,cb", [(4, "mul1"), (3, "mcg"), (6, "3inst")])
 def test_down_epilogue_bits_decode_pair(torch_cuda, bits, cb):
-    """The decode path's down (k_dn): 24 tokens top-4 over 48 experts, two classes, dropped slots."""
-    case = Case(seed=3100 + bits, n_tok=24, top_k=4, n_expert=48, geoms=[(512, 256), (512, 128)], bits=bits, cb=cb,
+    """The decode path's down (k_dn): 12 tokens top-4 over 48 experts, two classes, dropped slots."""
+    import exl3c4
+    case = Case(seed=3100 + bits, n_tok=12, top_k=4, n_expert=48, geoms=[(512, 256), (512, 128)], bits=bits, cb=cb,
                 drop=0.05)
-    assert case.T < 64 or case.T < 8 * case.n_expert    # the decode path
+    assert not exl3c4.is_prefill(case.T, case.n_expert)  # the decode path
     dev = Dev(case)
     h = dev.gate_up(h_rot=1)
     y = dev.down(h, h_rot=1)
@@ -68,10 +69,10 @@ def test_down_epilogue_bits_decode_pair(torch_cuda, bits, cb):
 
 
 def test_down_epilogue_bits_single_kernel_layer_geometry(torch_cuda):
-    """gate_up_down's single kernel (k_gd) at the decode layer's shapes: 8 tokens top-10 over 96 experts, K = 4."""
+    """gate_up_down's single kernel (k_gd) at the decode layer's shapes: 8 tokens top-10 over 128 experts, K = 4."""
     import exl3c4
-    case = Case(seed=3110, n_tok=8, top_k=10, n_expert=96, geoms=[(2048, 512)], bits=4, cb="mul1")
-    assert case.T >= exl3c4.GD_FUSE_MIN_T
+    case = Case(seed=3110, n_tok=8, top_k=10, n_expert=128, geoms=[(2048, 512)], bits=4, cb="mul1")
+    assert case.T >= exl3c4.GD_FUSE_MIN_T and not exl3c4.is_prefill(case.T, case.n_expert)
     dev = Dev(case)
     y = dev.gate_up_down()
     assert dev.status == 0
@@ -82,7 +83,7 @@ def test_down_epilogue_bits_single_kernel_layer_geometry(torch_cuda):
 @pytest.mark.parametrize("k_gu,k_dn", [(4, 8), (8, 3)])
 def test_down_epilogue_bits_single_kernel_mixed_k(torch_cuda, k_gu, k_dn):
     """k_gd with down's K apart from gate_up's (two of the 48-layer stack's pairs)."""
-    case = Case(seed=3120 + k_gu + k_dn, n_tok=8, top_k=10, n_expert=64, geoms=[(2048, 512)], bits=k_gu, cb="mul1",
+    case = Case(seed=3120 + k_gu + k_dn, n_tok=8, top_k=10, n_expert=128, geoms=[(2048, 512)], bits=k_gu, cb="mul1",
                 dn_bits=k_dn)
     dev = Dev(case)
     y = dev.gate_up_down()
@@ -93,9 +94,10 @@ def test_down_epilogue_bits_single_kernel_mixed_k(torch_cuda, k_gu, k_dn):
 
 def test_down_epilogue_bits_prefill(torch_cuda):
     """The prefill path's down GEMM (k_dn_pf): 512 tokens top-4 over 24 experts (Zipf), two classes, drops."""
+    import exl3c4
     case = Case(seed=3130, n_tok=512, top_k=4, n_expert=24, geoms=[(512, 256), (512, 128)], bits=4, cb="mul1",
                 drop=0.03, routing="zipf")
-    assert case.T >= 64 and case.T >= 8 * case.n_expert   # the prefill path
+    assert exl3c4.is_prefill(case.T, case.n_expert)       # the prefill path
     dev = Dev(case)
     h = dev.gate_up(h_rot=1)
     y = dev.down(h, h_rot=1)

@@ -107,7 +107,7 @@ FUSED = {
                       protect_tail=2),
     "two-class": dict(seed=51, n_tok=10, top_k=4, n_expert=12, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
                       drop=0.2),
-    "four-class-mcg": dict(seed=52, n_tok=8, top_k=8, n_expert=16,
+    "four-class-mcg": dict(seed=52, n_tok=7, top_k=8, n_expert=16,
                            geoms=[(256, 128), (256, 256), (128, 128), (256, 128)], bits=5, cb="mcg"),
     "chunks-of-many-rows": dict(seed=53, n_tok=20, top_k=2, n_expert=3, geoms=[(256, 128)], bits=3, cb="3inst",
                                 x_bf16=True),
@@ -118,7 +118,7 @@ FUSED = {
 def test_gate_up_down_as_one_kernel(torch_cuda, name):
     import exl3c4
     case = Case(**FUSED[name])
-    assert case.T >= exl3c4.GD_FUSE_MIN_T and (case.T < 64 or case.T < 8 * case.n_expert)
+    assert case.T >= exl3c4.GD_FUSE_MIN_T and not exl3c4.is_prefill(case.T, case.n_expert)
     dev = _check_all(case, f"one kernel {name}")
     assert dev.status == 0                             # the last launch (gate_up_down) ran as one kernel
 
@@ -138,13 +138,15 @@ def test_gate_up_down_as_one_kernel_at_the_layer_geometry(torch_cuda):
 
 
 # ------------------------------------------------------------------------------------------ the prefill path
-# (T >= 8 n_expert rows: chunks of up to 96 rows, a plan, the rotation into scratch, the prefill GEMMs)
+# (from exl3c4_prefill_min_rows(n_expert) sorted rows: chunks of up to 96 rows, a plan, the rotation into scratch, the
+# prefill GEMMs)
 def test_prefill_path_two_classes_several_chunks_with_drops(torch_cuda):
     """Runs of 126, 53, 111 and 63 rows: two experts cut into a full 96-row chunk (six row tiles, rows past 64 read
     their sorted_tok from the second register) and a short one, the others one chunk of 4 tiles."""
     case = Case(seed=40, n_tok=200, top_k=2, n_expert=4, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
                 drop=0.1, protect_tail=2, routing="zipf")
-    assert case.T >= 8 * case.n_expert and np.diff(case.off).max() > 96
+    import exl3c4
+    assert exl3c4.is_prefill(case.T, case.n_expert) and np.diff(case.off).max() > 96
     _check_all(case, "prefill two-class")
 
 
@@ -186,7 +188,7 @@ def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bit
     import exl3c4 as ex
     torch = torch_cuda
     ctr = None
-    for seed, n_tok, top_k, n_expert in ((70, 8, 10, 96), (71, 6, 8, 40), (72, 8, 10, 96), (73, 4, 8, 12)):
+    for seed, n_tok, top_k, n_expert in ((70, 8, 10, 128), (71, 6, 8, 40), (72, 8, 10, 128), (73, 4, 8, 12)):
         case = Case(seed=seed, n_tok=n_tok, top_k=top_k, n_expert=n_expert, geoms=[(512, 256)], bits=4, cb="mul1",
                     drop=0.05)
         dev = Dev(case)
@@ -210,9 +212,9 @@ def test_gate_up_down_with_a_counter_block_leaves_it_zero_and_gives_the_same_bit
 
 # ------------------------------------------------------------------------------------------ the gather in the op's kernel
 @pytest.mark.parametrize("seed,n_tok,top_k,n_expert,geoms,drop,empty", [
-    (80, 8, 10, 96, [(512, 256)], 0.05, False),                 # one kernel, dropped pairs
+    (80, 8, 10, 128, [(512, 256)], 0.05, False),                # one kernel, dropped pairs
     (81, 6, 8, 40, [(512, 256), (256, 128)], 0.0, False),       # two classes: the narrower one's blocks are zero
-    (82, 8, 10, 96, [(512, 256)], 0.0, True),                   # a token whose slots all drop
+    (82, 8, 10, 128, [(512, 256)], 0.0, True),                  # a token whose slots all drop
     (83, 5, 8, 12, [(256, 128)], 0.1, False),                   # few experts: chunks of several rows
     (84, 2, 8, 12, [(256, 128)], 0.0, False),                   # T = 16: two kernels, then the gather's own
     (85, 1, 2, 4, [(256, 128), (512, 256)], 0.0, False),       # T = 2: the smallest h formed by the epilogue kernel
@@ -276,7 +278,7 @@ def test_launch_gather_with_rows_past_t_leaves_the_counter_block_good(torch_cuda
     import exl3c4 as ex
     import oracle
     torch = torch_cuda
-    case = Case(seed=87, n_tok=8, top_k=10, n_expert=96, geoms=[(512, 256)], bits=4, cb="mul1")
+    case = Case(seed=87, n_tok=8, top_k=10, n_expert=128, geoms=[(512, 256)], bits=4, cb="mul1")
     dev = Dev(case)
     N = max(d["rows"] for d in dev.tabs["dn"])
     _, _, _, row_of = oracle.moe_scatter_full(case.ids, case.n_expert)

@@ -216,8 +216,9 @@ def test_gate_up_down_row_instance_counter_pool(torch_cuda):
     """The row instance's counter blocks: the same bits as exl3c4_launch, one block per (stream, output), each left
     zero; a launch whose block's flag says a wait gave up returns RAD_E_DEVICE, writes nothing, and the block serves
     the next launch normally."""
-    case = Case(seed=39, n_tok=8, top_k=10, n_expert=40, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
-    assert case.T >= 32
+    import exl3c4
+    case = Case(seed=39, n_tok=8, top_k=10, n_expert=112, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
+    assert case.T >= 32 and not exl3c4.is_prefill(case.T, case.n_expert)   # the single kernel: its counter blocks
     dev = Dev(case)
     p = Plug(dev)
     want = dev.gate_up_down()
@@ -253,8 +254,8 @@ def test_gate_up_down_row_instance_kernel_reports_a_wait_that_gave_up(torch_cuda
     flag (kernels/exl3r4d/exl3r4d.hip:1878-1880 raises the reference's). The block's next launch returns RAD_E_DEVICE
     and writes nothing; the one after it gives the good bits."""
     import exl3c4
-    case = Case(seed=41, n_tok=8, top_k=10, n_expert=40, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
-    assert case.T >= exl3c4.GD_FUSE_MIN_T
+    case = Case(seed=41, n_tok=8, top_k=10, n_expert=112, geoms=[(512, 256)], bits=4, cb="mul1", drop=0.05)
+    assert case.T >= exl3c4.GD_FUSE_MIN_T and not exl3c4.is_prefill(case.T, case.n_expert)
     dev = Dev(case)
     p = Plug(dev)
     want = dev.gate_up_down()

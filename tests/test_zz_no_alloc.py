@@ -43,7 +43,9 @@ def _both(dev, make):
 
 
 def test_noalloc_gives_the_launch_bits_on_two_calls_in_a_row_the_second_smaller(torch_cuda):
-    big = Case(seed=90, n_tok=8, top_k=10, n_expert=64, geoms=[(2048, 512)], bits=4, cb="mul1", drop=0.05)
+    import exl3c4 as ex
+    big = Case(seed=90, n_tok=8, top_k=10, n_expert=128, geoms=[(2048, 512)], bits=4, cb="mul1", drop=0.05)
+    assert not ex.is_prefill(big.T, big.n_expert)       # the decode path: gate_up_down's single kernel at 80 rows
     dev = Dev(big)
     for case, label in ((big, "8 tokens"), (big.rerouted(seed=91, n_tok=3, top_k=10), "3 tokens")):
         d = Dev(case, share=dev)
