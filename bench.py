@@ -266,6 +266,10 @@ def run_decode_layer(args, torch, exl3c4):
                                                     stream))
         check_rc(exl3c4, exl3c4.launch_ctr(layer_ops[i % n], scratch, ctr, stream))
         check_rc(exl3c4, exl3c4.moe_gather(y, True, w, row_of, out_t, stream))
+    if args.op_only:                                  # for a profiler's run: the op graph alone
+        ms_op = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch_ctr(ops[i % n], scratch, ctr, st)),
+                            args.steps, args.warmup)
+        return {"op_only": True, "op_us": round(ms_op / args.steps * 1e3, 2), "steps": args.steps}
     ms_sep = timed_graph(torch, layer_step_separate, args.steps, args.warmup)
     ms = timed_graph(torch, layer_step, args.steps, args.warmup)
     ms_op = timed_graph(torch, lambda i, st: check_rc(exl3c4, exl3c4.launch_ctr(ops[i % n], scratch, ctr, st)),
@@ -278,9 +282,13 @@ def run_decode_layer(args, torch, exl3c4):
     layer_gbps = float(np.mean(live)) * EXPERT_BYTES / (ms_step * 1e-3) / 1e9
     one = T >= exl3c4.GD_FUSE_MIN_T           # gate_up_down runs as one kernel: that kernel is the one timed
     durs = kernel_ms(torch, exl3c4, ops, scratch, exl3c4.K_GATE_UP_DOWN if one else exl3c4.K_GATE_UP, args.steps)
+    # the kernel's average launch duration as the layer runs it: the op graph's replay, back-to-back launches of the
+    # one kernel (a caller's zeroed counter block, no fill), events around the replay; beside it the eager launches'
+    # own event pairs (each dispatch behind a counter fill, stamped at its start and end)
+    avg_ms = ms_op / args.steps if one else float(np.mean(durs))
     # the kernel's algorithmic bytes: its live experts' packed codes and scale planes (perfmoe's definition)
     gemv_bytes = np.array(live, dtype=np.float64) * (EXPERT_BYTES if one else GU_CODE_BYTES)
-    gemv_gbps = float(np.mean(gemv_bytes) / (np.mean(durs) * 1e-3) / 1e9)
+    gemv_gbps = float(np.mean(gemv_bytes) / (avg_ms * 1e-3) / 1e9)
     kname = "k_gd_decode" if one else "k_gu_decode"
     # the memory floor of the same bytes: the step's live experts' planes read the way the kernel reads them
     floor = extent_read_floor(torch, layers, draws, n) if args.peaks else None
@@ -300,10 +308,13 @@ def run_decode_layer(args, torch, exl3c4):
         "roofline": {"bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": read_traffic(kname),
                      "kernel": "k_gd<4,mul1> (gate_up_down, one kernel)" if one else "k_gu<4,mul1> (gate_up GEMM)",
-                     "avg_us": round(float(np.mean(durs)) * 1e3, 3),
+                     "avg_us": round(avg_ms * 1e3, 3),
+                     "avg_us_how": ("graph replay of the op alone: back-to-back launches of its one kernel, events "
+                                    "around the replay" if one else "event pairs around each eager dispatch"),
+                     "avg_us_eager": round(float(np.mean(durs)) * 1e3, 3),
                      "bytes_per_launch": round(float(np.mean(gemv_bytes))),
                      "bytes_what": "live experts x (packed codes + suh, suh1, svh, dn_suh, dn_svh): 1,588,224 B each"},
-        "roofline_valu": valu_roofline(float(np.mean(live)), float(np.mean(durs)) * 1e-3),
+        "roofline_valu": valu_roofline(float(np.mean(live)), avg_ms * 1e-3),
         "cpu_baseline": cpu,
     })
     if floor:
@@ -648,6 +659,8 @@ def main():
                     help="configs[4]: run each mixed-K layer as gate_up then down (two ops) instead of one launch")
     ap.add_argument("--no-prefill", dest="prefill", action="store_false",
                     help="with the default decode layer: skip the prefill layer's figures")
+    ap.add_argument("--op-only", action="store_true",
+                    help="the decode layer's op graph alone (gate_up_down launches back to back), for a profiler")
     ap.add_argument("--no-stack", dest="stack", action="store_false",
                     help="with the default decode layer: skip the 48-layer stack's figures")
     ap.add_argument("--no-peaks", dest="peaks", action="store_false",
@@ -674,6 +687,9 @@ def main():
     torch.cuda.set_device(0)
     run = {2: run_single_expert, 3: run_decode_layer, 4: run_prefill_layer, 5: run_stack}[args.config]
     out = run(args, torch, exl3c4)
+    if out.get("op_only"):
+        print(json.dumps(out), flush=True)
+        return
     peaks = measured_peaks(torch) if args.peaks else None
     if args.config == 3 and args.prefill:
         # the prefill layer measured in the same run, its figures beside the decode line's
