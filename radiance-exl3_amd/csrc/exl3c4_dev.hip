@@ -40,6 +40,7 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short ushort2_t __attribute__((ext_vector_type(2)));
 typedef float    float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4a_t __attribute__((ext_vector_type(4), aligned(4)));
@@ -189,35 +190,26 @@ __device__ __forceinline__ Mul1Consts mul1_consts() {
 // state: h = x * 0x83DCD12D mod 2^32 = (x * 0x83DC mod 2^16) << 16 + x * 0xD12D -- v_pk_mul_lo_u16 puts the high
 // partial product in the high half over a zero low half (op_sel), v_mad_u32_u16 adds x * 0xD12D reading only the
 // state's half (op_sel), so no state is masked. Then v_sad_u8 / v_sad_hi_u8 leave 0x6400 + bytesum in each half
-// (fp16 1024 + s, exact), and one fp16x2 fma forms (1024 + s) * K_INV + K_BIAS for both, one rounding each.
-// The integer steps are one asm block (their op_sel half selects written out). The fma is ordinary code
-// (v_pk_fma_f16 by instruction selection): its result feeds an MFMA, which needs two wait states after the VALU
-// write of a source, and the compiler's hazard recognizer inserts them only for instructions it emitted itself,
-// never for an asm block's outputs.
-#define EXL3C4_MUL1_PAIR(HA, HB)                                                                            \
-    "v_pk_mul_lo_u16 %[ya], %[ra], %[kh] op_sel:[" #HA ",0] op_sel_hi:[" #HA ",1]\n\t"                    \
-    "v_pk_mul_lo_u16 %[yb], %[rb], %[kh] op_sel:[" #HB ",0] op_sel_hi:[" #HB ",1]\n\t"                    \
-    "v_mad_u32_u16 %[ya], %[ra], %[cl], %[ya] op_sel:[" #HA ",0,0,0]\n\t"                                 \
-    "v_mad_u32_u16 %[yb], %[rb], %[cl], %[yb] op_sel:[" #HB ",0,0,0]\n\t"                                 \
-    "v_sad_u8 %[ya], %[ya], 0, %[c64]\n\t"                                                                \
-    "v_sad_hi_u8 %[ya], %[yb], 0, %[ya]"
-
-__device__ __forceinline__ uint32_t mul1_fma(uint32_t s, const Mul1Consts& k) {
-    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, s), k.kinv, k.kbias));
+// (fp16 1024 + s, exact), and one v_pk_fma_f16 forms (1024 + s) * K_INV + K_BIAS for both, one rounding each.
+// Only the two v_mad_u32_u16 are asm (their op_sel half select is not reached from ordinary code, which spends a
+// shift or a mask on it), and they rewrite registers the compiler's own v_pk_mul_lo_u16 defined: the compiler keeps
+// every register an MFMA reads in its hazard windows -- a VALU write of an MFMA source needs two wait states before
+// the MFMA reads it, and one of a source C the MFMA has read needs three -- only for instructions it emitted, so no
+// asm output may be a register first written by the asm or a value an MFMA reads.
+template <int H> __device__ __forceinline__ uint32_t mul1_hi_product(uint32_t r, uint32_t kh) {
+    const ushort2_t v = __builtin_bit_cast(ushort2_t, r);
+    return __builtin_bit_cast(uint32_t, __builtin_shufflevector(v, v, H, H) * __builtin_bit_cast(ushort2_t, kh));
 }
 
 template <int HA, int HB>
 __device__ __forceinline__ uint32_t mul1_pair(uint32_t ra, uint32_t rb, const Mul1Consts& k) {
-    uint32_t ya, yb;
-#define EXL3C4_ARGS                                                                                          \
-    : [ya] "=&v"(ya), [yb] "=&v"(yb)                                                                        \
-    : [ra] "v"(ra), [rb] "v"(rb), [kh] "s"(k.kh), [cl] "s"(k.cl), [c64] "s"(k.c6464)
-    if constexpr (HA == 0 && HB == 0) asm(EXL3C4_MUL1_PAIR(0, 0) EXL3C4_ARGS);
-    else if constexpr (HA == 0 && HB == 1) asm(EXL3C4_MUL1_PAIR(0, 1) EXL3C4_ARGS);
-    else if constexpr (HA == 1 && HB == 0) asm(EXL3C4_MUL1_PAIR(1, 0) EXL3C4_ARGS);
-    else asm(EXL3C4_MUL1_PAIR(1, 1) EXL3C4_ARGS);
-#undef EXL3C4_ARGS
-    return mul1_fma(ya, k);
+    uint32_t ya = mul1_hi_product<HA>(ra, k.kh), yb = mul1_hi_product<HB>(rb, k.kh);
+    asm("v_mad_u32_u16 %[ya], %[ra], %[cl], %[ya] op_sel:[%c[ha],0,0,0]\n\t"
+        "v_mad_u32_u16 %[yb], %[rb], %[cl], %[yb] op_sel:[%c[hb],0,0,0]"
+        : [ya] "+v"(ya), [yb] "+v"(yb)
+        : [ra] "v"(ra), [rb] "v"(rb), [cl] "s"(k.cl), [ha] "n"(HA), [hb] "n"(HB));
+    const uint32_t s = __builtin_amdgcn_sad_hi_u8(yb, 0u, __builtin_amdgcn_sad_u8(ya, 0u, k.c6464));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2_t, s), k.kinv, k.kbias));
 }
 
 // mcg / 3inst (common/exl3_decode.c:59-66): a 32-bit hash, (h & 0x8FFF8FFF) ^ 0x3B603B60, fp16 lo + hi rounded once.
