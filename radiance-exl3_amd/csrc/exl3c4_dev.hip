@@ -1723,41 +1723,69 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     pf_gemm<BITS, CB, 1>(D.codes, D.codes_s, D.cols, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0,
                          lds, acc);
 
+    // The epilogue, a tile's 16 rows at a time: the sums cross LDS, then wave w takes the tile's rows 4 w .. 4 w + 3,
+    // a 16-lane row of the wave per row, lane l holding the 8 consecutive columns 8 g .. 8 g + 7 of the block
+    // (g = rot_group(l & 15)) -- had128_x8's layout: its stages h = 1, 2, 4 inside the lane, h = 8 .. 64 one DPP
+    // v_fmac each within the 16-lane row -- then x svh, bf16, and one 16-byte store a lane.
     const void* svh = tab_entry(D.svh, D.svh_s, jx);
-    const int el = had_col(lane), et = had_col_t(lane);          // the block's sums' columns, its outputs'
-    const uint16_t sv0 = ldg16(svh, b * 128 + et), sv1 = ldg16(svh, b * 128 + 64 + et);
-    float* acc_l = (float*)lds;                                   // [16][128], one row tile at a time
+    const int g = rot_group(lane & 15), gcol = b * 128 + 8 * g;   // the lane's first column in y
+    const RotSigns ks = rot_signs(g);
+    float sv[8];
+    {
+        uint32_t s4[4];
+        load8w((const uint16_t*)svh + gcol, (((uintptr_t)svh) & 15) == 0, s4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sv[2 * j] = h2f((uint16_t)s4[j]);
+            sv[2 * j + 1] = h2f((uint16_t)(s4[j] >> 16));
+        }
+    }
+    const bool yw = ((((uintptr_t)a.y) | ((uintptr_t)a.y_pitch * 2)) & 15) == 0;
+    constexpr int EP = 132;                                       // floats a staged row: 16-byte rows off one bank
+    float* acc_l = (float*)lds;                                   // [16][EP], one row tile at a time
     const int cc = lane & 15, rg = lane >> 4;
     const int col = 32 * wave + 16 * (cc & 1) + (cc >> 1);
     const int ntile = (nrows + 15) >> 4;
+    const int lrow = 4 * wave + (lane >> 4);                      // this lane's row of a tile
 #pragma unroll
     for (int t = 0; t < PF_NT; ++t) {                             // unrolled: acc[t] stays in registers
         if (t >= ntile) break;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            acc_l[(rg * 4 + q) * 128 + col] = acc[t][0][q];
-            acc_l[(rg * 4 + q) * 128 + col + 8] = acc[t][1][q];
+            acc_l[(rg * 4 + q) * EP + col] = acc[t][0][q];
+            acc_l[(rg * 4 + q) * EP + col + 8] = acc[t][1][q];
         }
         __syncthreads();
-        for (int q = wave; q < 16; q += 4) {
-            const int row = t * 16 + q;
+        if (t * 16 + 4 * wave < nrows) {                          // uniform: the wave holds a row of the chunk
+            const int row = t * 16 + lrow;                        // rows past the chunk: computed, not stored
+            const float4_t lo = *(const float4_t*)(acc_l + lrow * EP + 8 * g);
+            const float4_t hi = *(const float4_t*)(acc_l + lrow * EP + 8 * g + 4);
+            float v[8] = { lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3] };
+            const int tk_lo = __shfl(srt, row & 63), tk_hi = __shfl(srt2, row & 63);
+            const int tk = row < 64 ? tk_lo : tk_hi;
+            had128_x8(v, ks);
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = tk < 0 ? 0u : f2bf2(v[2 * j] * sv[2 * j], v[2 * j + 1] * sv[2 * j + 1]);
             if (row < nrows) {
                 const int64_t r = row0 + row;
-                float y0 = acc_l[q * 128 + el], y1 = acc_l[q * 128 + el + 64];
                 if (a.keep_sums) {
-                    float* dacc = a.dacc + r * a.dacc_pitch + b * 128;
-                    dacc[el] = y0;
-                    dacc[el + 64] = y1;
+                    float* dacc = a.dacc + r * a.dacc_pitch + gcol;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        dacc[j] = lo[j];
+                        dacc[4 + j] = hi[j];
+                    }
                 }
-                uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + b * 128;
-                if ((row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64)) < 0) {
-                    out[el] = 0;
-                    out[el + 64] = 0;
+                uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + gcol;
+                if (yw) {
+                    *(uint4*)out = uint4{ o[0], o[1], o[2], o[3] };
                 } else {
-                    had128_wave<false>(y0, y1, lane);
-                    const uint32_t yb = f2bf2(y0 * h2f(sv0), y1 * h2f(sv1));
-                    out[et] = (uint16_t)yb;
-                    out[et + 64] = (uint16_t)(yb >> 16);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        out[2 * j] = (uint16_t)o[j];
+                        out[2 * j + 1] = (uint16_t)(o[j] >> 16);
+                    }
                 }
             }
         }
