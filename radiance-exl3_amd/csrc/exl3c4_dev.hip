@@ -1646,14 +1646,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int cc = lane & 15, rg = lane >> 4;
     const int n = strip * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
     const int col_l = half * 128 + (wave & 3) * EXL3C4_STRIP + 16 * (cc & 1) + (cc >> 1);
-    const void* svh = tab_entry(K.svh, K.svh_s, jx);
-    const void* ds = a.h_rot ? tab_entry(K.dn_suh, K.dn_suh_s, jx) : nullptr;
-    const int el = had_col(lane), n0 = hb * 128 + had_col_t(lane), n1 = n0 + 64;   // the scales' columns
-    const int eo = a.h_rot ? el : had_col_t(lane);                                  // h's columns
-    const uint16_t sg0 = ldg16(svh, n0), sg1 = ldg16(svh, n1), su0 = ldg16(svh, width + n0), su1 = ldg16(svh, width + n1);
-    const uint16_t d0 = a.h_rot ? ldg16(ds, n0) : 0, d1 = a.h_rot ? ldg16(ds, n1) : 0;
+    // The epilogue in had128_x8's layout: the accumulations cross LDS EPI_T row tiles at a time, then the waves take
+    // the pass's rows four at a time, a 16-lane row of the wave per row, lane l holding the 8 consecutive columns
+    // 8 g .. 8 g + 7 of the block (g = rot_group(l & 15)) of gate and of up: had128, x svh, f16(silu(gate) * up), and
+    // with h_rot f16(had(f16(h * dn_suh))), the reference's steps and roundings (gate_up_math's, in another lane
+    // layout), then one 16-byte store a lane.
+    const int g = rot_group(lane & 15), gcol = hb * 128 + 8 * g;  // the lane's first column of the block
+    const RotSigns ks = rot_signs(g);
+    uint32_t sg[4], su[4], sd[4];                                 // svh (gate, up) and dn_suh of those columns
+    {
+        const uint16_t* svh = (const uint16_t*)tab_entry(K.svh, K.svh_s, jx);
+        const bool sw = (((uintptr_t)svh) & 15) == 0 && (width & 7) == 0;
+        load8w(svh + gcol, sw, sg);
+        load8w(svh + width + gcol, sw, su);
+        if (a.h_rot) {
+            const uint16_t* ds = (const uint16_t*)tab_entry(K.dn_suh, K.dn_suh_s, jx);
+            load8w(ds + gcol, (((uintptr_t)ds) & 15) == 0, sd);
+        } else {
+            sd[0] = sd[1] = sd[2] = sd[3] = 0;
+        }
+    }
+    const bool yw = ((((uintptr_t)a.y) | ((uintptr_t)a.y_pitch * 2)) & 15) == 0;
     float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
-    // The accumulations cross LDS EPI_T row tiles at a time; each wave then finishes whole rows of the block.
 #pragma unroll
     for (int p = 0; p < PF_NT / EPI_T; ++p) {
         const int r0 = p * EPI_T * 16;                            // the pass's first chunk row
@@ -1674,18 +1688,48 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 }
             }
         __syncthreads();
-        for (int row = r0 + wave; row < min(nrows, r0 + EPI_T * 16); row += 8) {
-            const int64_t r = row0 + row;
-            uint16_t v0 = 0, v1 = 0;
-            const int st = row < 64 ? __builtin_amdgcn_readlane(srt, row) : __builtin_amdgcn_readlane(srt2, row - 64);
-            if (st >= 0) {
-                const float* pp = acc_l + (row - r0) * ACC_PITCH;
-                const float ac[4] = { pp[el], pp[el + 64], pp[128 + el], pp[192 + el] };
-                gate_up_math(ac, sg0, sg1, su0, su1, d0, d1, a.h_rot, lane, v0, v1);
+        const int rend = min(nrows, r0 + EPI_T * 16);
+        for (int rb = r0 + 4 * wave; rb < rend; rb += 32) {       // uniform: the wave's four rows start in the pass
+            const int row = rb + (lane >> 4);                     // rows past the pass: computed, not stored
+            const float* pp = acc_l + (min(row, r0 + EPI_T * 16 - 1) - r0) * ACC_PITCH + 8 * g;
+            const float4_t g_lo = *(const float4_t*)pp, g_hi = *(const float4_t*)(pp + 4);
+            const float4_t u_lo = *(const float4_t*)(pp + 128), u_hi = *(const float4_t*)(pp + 132);
+            float gv[8] = { g_lo[0], g_lo[1], g_lo[2], g_lo[3], g_hi[0], g_hi[1], g_hi[2], g_hi[3] };
+            float uv[8] = { u_lo[0], u_lo[1], u_lo[2], u_lo[3], u_hi[0], u_hi[1], u_hi[2], u_hi[3] };
+            const int tk_lo = __shfl(srt, row & 63), tk_hi = __shfl(srt2, row & 63);
+            const int tk = row < 64 ? tk_lo : tk_hi;
+            had128_x8(gv, ks);
+            had128_x8(uv, ks);
+            uint16_t hv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float gs = gv[j] * h2f((uint16_t)(sg[j >> 1] >> (16 * (j & 1))));
+                const float us = uv[j] * h2f((uint16_t)(su[j >> 1] >> (16 * (j & 1))));
+                hv[j] = f2h(silu(gs) * us);
             }
-            uint16_t* out = (uint16_t*)a.y + r * a.y_pitch + hb * 128;
-            out[eo] = v0;
-            out[eo + 64] = v1;
+            if (a.h_rot) {
+                float rv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) rv[j] = h2f(f2h(h2f(hv[j]) * h2f((uint16_t)(sd[j >> 1] >> (16 * (j & 1))))));
+                had128_x8(rv, ks);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) hv[j] = f2h(rv[j]);
+            }
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = tk < 0 ? 0u : ((uint32_t)hv[2 * j] | ((uint32_t)hv[2 * j + 1] << 16));
+            if (row < rend) {
+                uint16_t* out = (uint16_t*)a.y + (int64_t)(row0 + row) * a.y_pitch + gcol;
+                if (yw) {
+                    *(uint4*)out = uint4{ o[0], o[1], o[2], o[3] };
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        out[2 * j] = (uint16_t)o[j];
+                        out[2 * j + 1] = (uint16_t)(o[j] >> 16);
+                    }
+                }
+            }
         }
     }
 }
