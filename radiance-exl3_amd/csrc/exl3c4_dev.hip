@@ -158,6 +158,29 @@ template <bool T_IN> __device__ __forceinline__ void had128_wave(float& v0, floa
 // one round of independent loads and a wave reduction, checked against off[e] <= i < off[e + 1] (-1 otherwise). A
 // dependent binary search costs one memory latency per halving; this costs about one in all.
 __device__ __forceinline__ int owner_wave(const int32_t* off, int n_expert, int i, int lane) {
+    constexpr int OJ = 9;                                         // up to 575 experts: one round of loads
+    if (n_expert < 64 * OJ) {
+        // off[0 .. n_expert] held by the wave (lane l, register j: e = l + 64 j, past n_expert a copy of the last),
+        // loaded at once; the owner's number counted by ballots (a scalar result); off[e] and off[e + 1] then read
+        // out of the registers, not loaded again
+        int o[OJ];
+#pragma unroll
+        for (int j = 0; j < OJ; ++j) o[j] = off[min(lane + 64 * j, n_expert)];
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < OJ; ++j) {
+            const int e = lane + 64 * j;
+            cnt += __popcll(__ballot(e >= 1 && e <= n_expert && o[j] <= i));
+        }
+        const int e = min(cnt, n_expert - 1);
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < OJ; ++j) {                            // uniform tests: the registers that hold them
+            if ((e >> 6) == j) lo = __builtin_amdgcn_readlane(o[j], e & 63);
+            if (((e + 1) >> 6) == j) hi = __builtin_amdgcn_readlane(o[j], (e + 1) & 63);
+        }
+        return (lo <= i && i < hi) ? e : -1;
+    }
     int cnt = 0;
 #pragma unroll 8
     for (int e = 1 + lane; e <= n_expert; e += 64) cnt += off[e] <= i ? 1 : 0;
@@ -1372,8 +1395,9 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const int i = __builtin_amdgcn_readfirstlane(wg * 4 + (int)(threadIdx.x >> 6));
     if (wg >= nwg || i >= a.T) return;
     const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
+    const int tok_v = a.sorted[i];                                // out with the owner search's loads
     const int e = __builtin_amdgcn_readfirstlane(owner_wave(a.off, a.n_expert, i, lane));   // the plan writes row_info
-    const int tok = a.sorted[i];
+    const int tok = __builtin_amdgcn_readfirstlane(tok_v);       // uniform: the row's addresses are scalar
     if (e < 0) return;
     const Exl3c4DevClass& K = a.cls[class_of(a, e)];
     const int64_t jx = entry_of(a, e);
