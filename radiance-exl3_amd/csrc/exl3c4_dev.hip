@@ -1344,9 +1344,10 @@ __device__ __forceinline__ RotSigns rot_signs(int g) {
     return RotSigns{ (g & 1) ? -1.f : 1.f, (g & 2) ? -1.f : 1.f, (g & 4) ? -1.f : 1.f, (g & 8) ? -1.f : 1.f,
                      (__builtin_popcount(g) & 1) ? -kHadScale : kHadScale };
 }
+template <int H0 = 1>                                             // the first in-lane stage not yet done
 __device__ __forceinline__ void had128_x8(float (&v)[8], const RotSigns& k) {
 #pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
+    for (int h = H0; h < 8; h <<= 1)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (!(j & h)) {
@@ -1381,6 +1382,64 @@ __device__ __forceinline__ void load8w(const uint16_t* p, bool wide, uint32_t (&
 // to the XCDs in contiguous ranges, so a run's rows (one expert's scales) share an L2. Rows no run holds are not
 // written (nothing reads them); a negative sorted_tok gives zeros.
 constexpr int ROT_PASSES = 2;
+// f32 (lo of w) + f32 (hi of w) and f32 (lo) - f32 (hi) of a dword of two f16 values: each one v_fma_mix_f32 (the f16
+// sources taken exactly, one rounding), the first butterfly stage of two neighbours straight from their packed f16
+// product -- as the f16 -> f32 conversions then an f32 add and subtract would round them.
+__device__ __forceinline__ void mix_sum_diff(uint32_t w, float& sum, float& dif) {
+    asm("v_fma_mix_f32 %0, %2, 1.0, %2 op_sel:[0,0,1] op_sel_hi:[1,0,1]\n\t"
+        "v_fma_mix_f32 %1, %2, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[1,0,1]"
+        : "=&v"(sum), "=v"(dif) : "v"(w));
+}
+
+// One row's passes: per pass each lane's 8 consecutive columns of each half (BF: x in bf16), as described at k_rot.
+template <bool BF, int HALVES>
+__device__ __forceinline__ void rot_passes(const uint16_t* x, const uint16_t* s0, const uint16_t* s1, uint16_t* out,
+                                           int C, int npass, int lcol, int g, bool xw, bool sw, const RotSigns& ks) {
+    for (int p0 = 0; p0 < npass; p0 += ROT_PASSES) {
+        uint32_t xq[ROT_PASSES][4], sq[2][ROT_PASSES][4];
+#pragma unroll
+        for (int q = 0; q < ROT_PASSES; ++q) {
+            int col = (p0 + q) * 512 + lcol;
+            col = col < C ? col : 8 * g;                            // past the row: reload the first block (unused)
+            load8w(x + col, xw, xq[q]);
+            load8w(s0 + col, sw, sq[0][q]);
+            if (HALVES == 2) load8w(s1 + col, sw, sq[1][q]);
+        }
+#pragma unroll
+        for (int m = 0; m < HALVES; ++m) {
+#pragma unroll
+            for (int q = 0; q < ROT_PASSES; ++q) {
+                if (p0 + q >= npass) break;
+                float v[8];
+                if (BF) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t xb = xq[q][j], sb = sq[m][q][j];
+                        v[2 * j] = h2f(f2h(bf2f((uint16_t)xb) * h2f((uint16_t)sb)));
+                        v[2 * j + 1] = h2f(f2h(bf2f((uint16_t)(xb >> 16)) * h2f((uint16_t)(sb >> 16))));
+                    }
+                    had128_x8(v, ks);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const half2_t pr = __builtin_bit_cast(half2_t, xq[q][j]) * __builtin_bit_cast(half2_t, sq[m][q][j]);
+                        mix_sum_diff(__builtin_bit_cast(uint32_t, pr), v[2 * j], v[2 * j + 1]);   // stage h = 1
+                    }
+                    had128_x8<2>(v, ks);
+                }
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    typedef float float2v __attribute__((ext_vector_type(2)));
+                    const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
+                    o[j] = __builtin_bit_cast(uint32_t, hv);
+                }
+                const int col = (p0 + q) * 512 + lcol;
+                if (col < C) *(uint4*)(out + m * C + col) = uint4{ o[0], o[1], o[2], o[3] };
+            }
+        }
+    }
+}
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     if (a.plan && blockIdx.x == 0) {                              // the launch's first workgroup plans the GEMMs
         plan_body<256>(a);
@@ -1420,48 +1479,11 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     const uint16_t* s1 = halves == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_s, jx) : s0;
     const bool xw = (((uintptr_t)a.x | (uintptr_t)(a.x_pitch * 2)) & 15) == 0;
     const bool sw = (((uintptr_t)s0 | (uintptr_t)s1) & 15) == 0;
-    const bool bf = halves == 2 && a.x_dtype == EXL3C4_BF16;
-    for (int p0 = 0; p0 < npass; p0 += ROT_PASSES) {
-        uint32_t xq[ROT_PASSES][4], sq[2][ROT_PASSES][4];
-#pragma unroll
-        for (int q = 0; q < ROT_PASSES; ++q) {
-            int col = (p0 + q) * 512 + lcol;
-            col = col < C ? col : 8 * g;                            // past the row: reload the first block (unused)
-            load8w(x + col, xw, xq[q]);
-            load8w(s0 + col, sw, sq[0][q]);
-            if (halves == 2) load8w(s1 + col, sw, sq[1][q]);
-        }
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            if (m >= halves) break;
-#pragma unroll
-            for (int q = 0; q < ROT_PASSES; ++q) {
-                if (p0 + q >= npass) break;
-                float v[8];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (bf) {
-                        const uint32_t xb = xq[q][j], sb = sq[m][q][j];
-                        v[2 * j] = h2f(f2h(bf2f((uint16_t)xb) * h2f((uint16_t)sb)));
-                        v[2 * j + 1] = h2f(f2h(bf2f((uint16_t)(xb >> 16)) * h2f((uint16_t)(sb >> 16))));
-                    } else {
-                        const half2_t pr = __builtin_bit_cast(half2_t, xq[q][j]) * __builtin_bit_cast(half2_t, sq[m][q][j]);
-                        v[2 * j] = (float)pr.x;
-                        v[2 * j + 1] = (float)pr.y;
-                    }
-                }
-                had128_x8(v, ks);
-                uint32_t o[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    typedef float float2v __attribute__((ext_vector_type(2)));
-                    const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
-                    o[j] = __builtin_bit_cast(uint32_t, hv);
-                }
-                const int col = (p0 + q) * 512 + lcol;
-                if (col < C) *(uint4*)(out + m * C + col) = uint4{ o[0], o[1], o[2], o[3] };
-            }
-        }
+    if (halves == 2) {
+        if (a.x_dtype == EXL3C4_BF16) rot_passes<true, 2>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
+        else rot_passes<false, 2>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
+    } else {
+        rot_passes<false, 1>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
     }
 }
 
