@@ -442,8 +442,8 @@ def measured_peaks(torch):
     """What this box reaches, on this library's own kernels (libexl3c4_calib.so, event-timed, best of 8): HBM read (a
     4 GiB stream, 16-byte loads, four in flight a thread), the VALU issue rate of the trellis decode's own
     instructions (8 independent chains a wave, 4 to 8 waves a SIMD) and with it the engine clock under that load, and
-    the f16 MFMA rate (v_mfma_f32_16x16x32_f16, 8 independent chains a wave); beside them torch's plain copy and
-    hipBLASLt's f16 GEMM (library work)."""
+    the f16 MFMA rate (v_mfma_f32_16x16x32_f16, 8 independent chains a wave); beside them torch's plain copy and fill
+    and hipBLASLt's f16 GEMM (library work)."""
     C = calib()
     st = torch.cuda.current_stream().cuda_stream
     n = 1 << 30
@@ -466,6 +466,7 @@ def measured_peaks(torch):
         return min(ts)
     y = torch.empty_like(x)
     copy_gbps = 8.0 * n / (best_ms(lambda: y.copy_(x)) * 1e-3) / 1e9
+    fill_gbps = 4.0 * n / (best_ms(lambda: y.fill_(1.0)) * 1e-3) / 1e9          # write-only: k_rot's xr traffic
     del x, y
     rounds = 2000
     valu = []
@@ -486,12 +487,13 @@ def measured_peaks(torch):
     gemm_tflops = 2.0 * m ** 3 / (best_ms(lambda: torch.matmul(a, b), 6) * 1e-3) / 1e12
     del a, b
     torch.cuda.empty_cache()
-    return {"hbm_read_GBps": round(read, 1), "hbm_copy_GBps": round(copy_gbps, 1),
+    return {"hbm_read_GBps": round(read, 1), "hbm_copy_GBps": round(copy_gbps, 1), "hbm_fill_GBps": round(fill_gbps, 1),
             "valu_Ginstr_s": round(valu_g, 1), "valu_clock_GHz": round(valu_g * 4 / 1024, 3),
             "mfma_f16_TFLOPs": round(max(mfma), 1), "fp16_gemm_TFLOPs": round(gemm_tflops, 1),
             "how": ("best of 8 event-timed launches: libexl3c4_calib.so k_read over 4 GiB (hbm_read), k_valu (the "
                     "mul1 pair's 7 instructions x 8 chains a wave; clock = rate x 4 cycles / 1024 SIMDs), k_mfma "
-                    "(v_mfma_f32_16x16x32_f16 x 8 chains a wave); torch copy_ of 4 GiB (read + write bytes); "
+                    "(v_mfma_f32_16x16x32_f16 x 8 chains a wave); torch copy_ of 4 GiB (read + write bytes); torch fill_ "
+                    "of 4 GiB (write-only); "
                     "torch.matmul f16 8192^3 (hipBLASLt)")}
 
 
