@@ -156,6 +156,19 @@ def test_prefill_path_four_classes_mcg(torch_cuda):
     _check_all(case, "prefill four-class")
 
 
+@pytest.mark.parametrize("n_expert", [575, 576, 600])
+def test_owner_search_on_both_sides_of_its_one_round_form(torch_cuda, n_expert):
+    """The rotation kernels' owner search (k_prep's and k_rot's) holds the run offsets of up to 575 experts in one round
+    of loads and reads the owner's run bounds out of its registers; from 576 experts it loops over the offsets and
+    loads the bounds again. 480 sorted rows over 575, 576 and 600 experts (the prefill path: T >= 3/4 n_expert), with
+    dropped slots, through every op against the oracle."""
+    import exl3c4
+    case = Case(seed=45 + n_expert, n_tok=120, top_k=4, n_expert=n_expert, geoms=[(256, 128)], bits=4, cb="mul1",
+                drop=0.05)
+    assert exl3c4.is_prefill(case.T, case.n_expert)
+    _check_all(case, f"owner search, {n_expert} experts")
+
+
 def test_prefill_path_bf16_3inst(torch_cuda):
     _check_all(Case(seed=42, n_tok=64, top_k=1, n_expert=2, geoms=[(256, 128)], bits=3, cb="3inst", x_bf16=True),
                "prefill bf16")
