@@ -111,30 +111,47 @@ static const RadOperandSpec o_gd4[] = {
 
 #define N_OF(a) (int)(sizeof(a) / sizeof((a)[0]))
 /* schema order: 0 gate_up, 1 down, 2 prep_gu, 3 gate_up_down, then their four-class forms */
+/* The schemas' doc strings are the reference's own text (include/exl3_abi.h:590-625), kept verbatim: the engine's loader
+ * compares the schemas of the libraries that implement these ops and refuses a second one that declares them
+ * differently (docs/OPS.md:139-150 at radiance 1.3.0), and `rad-schemas exl3ref.so <this>.so` is meant to print no
+ * difference. The tests compare them with the header's text. */
 static const RadOpSchema k_schema[8] = {
     { "moe_exl3_gate_up", p_gu, N_OF(p_gu), o_gu, N_OF(o_gu),
-      "EXL3 routed experts, gate and up: per sorted row the token's activations scaled by suh (suh1 for up) and "
-      "Hadamard-128 rotated (or, a_rot = 1, prep_gu's xr as given), times W_hat, rotated back, scaled by svh, "
-      "f16(silu(gate) * up); h_rot = 1 adds down's first step (x dn_suh, rotated). Two parity classes of experts, "
-      "expert e at entry e / 2 of class e % 2; rows no run holds are zero." },
+      "EXL3 routed experts, gate and up: per sorted row, a[sorted_tok/top_k] scaled by suh (suh.1 for up) "
+      "and rotated, times W_hat, rotated back and scaled by svh, then f16(silu(gate) * up); with h_rot = 1 "
+      "that then scaled by down's suh (dn_suh) and rotated, which is down's first step; with a_rot = 1 `a` "
+      "is moe_exl3_prep_gu's xr and the input rotation is not redone. One weight table a plane a parity "
+      "class, expert e at entry e/2; rows past expert_offset[n_expert] are zero. expert_w is not applied. "
+      "docs/OPS-exl3.md." },
     { "moe_exl3_down", p_dn, N_OF(p_dn), o_dn, N_OF(o_dn),
-      "EXL3 routed experts, down: per sorted row h scaled by suh and rotated (h_rot = 1: as given), times W_hat, "
-      "rotated back, scaled by svh, bf16. Two parity classes; rows no run holds are zero." },
+      "EXL3 routed experts, down: per sorted row, h[i] scaled by suh and rotated (with h_rot = 1: h[i] as "
+      "gate_up already rotated it), times W_hat, rotated back and scaled by svh, bf16. One weight table a "
+      "plane a parity class, expert e at entry e/2; rows past expert_offset[n_expert] are zero. expert_w is"
+      " not applied. docs/OPS-exl3.md." },
     { "moe_exl3_prep_gu", p_pg, N_OF(p_pg), o_pg, N_OF(o_pg),
-      "EXL3 routed experts, gate_up's input rotation as an op: per sorted row the token's activations x suh and x "
-      "suh1, each rotated, side by side in xr f16 [T, 2 max(K, K_odd)]." },
+      "EXL3 routed experts, gate_up's input rotation as an op: per sorted row, a[sorted_tok/top_k] scaled "
+      "by suh and rotated, then by suh.1 and rotated, side by side (xr, f16 [T, 2*max(K, K_odd)]) -- what "
+      "moe_exl3_gate_up with a_rot = 1 reads. Rows past expert_offset[n_expert] are zero. docs/OPS-exl3.md." },
     { "moe_exl3_gate_up_down", p_gd, N_OF(p_gd), o_gd, N_OF(o_gd),
-      "EXL3 routed experts, the decode chain as one op: moe_exl3_down(h_rot = 1) of moe_exl3_gate_up(a_rot = 0, "
-      "h_rot = 1), to the bit; dn_suh / dn_codes / dn_svh are down's planes ([K, N / 2])." },
+      "EXL3 routed experts, the decode chain as one op: y = moe_exl3_down(h_rot = 1) of "
+      "moe_exl3_gate_up(a_rot = 0, h_rot = 1) of a, on the same routing; dn_suh / dn_codes / dn_svh are "
+      "down's planes ([K, N/2]); h and the rotated input are scratch. Rows past expert_offset[n_expert] are"
+      " zero. docs/OPS-exl3.md." },
     { "moe_exl3_gate_up_mod4", p_gu4, N_OF(p_gu4), o_gu4, N_OF(o_gu4),
-      "moe_exl3_gate_up over four classes of experts by number mod 4: class q [N_q, K_q], expert e at entry e / 4 "
-      "of class e % 4." },
+      "moe_exl3_gate_up over FOUR classes of experts by number mod 4 (moe_gemm_q_mod4's): class q at [N_q, "
+      "K_q], expert e at entry e/4 of class e%4; otherwise moe_exl3_gate_up. docs/OPS-exl3.md." },
     { "moe_exl3_down_mod4", p_dn4, N_OF(p_dn4), o_dn4, N_OF(o_dn4),
-      "moe_exl3_down over four classes of experts by number mod 4." },
+      "moe_exl3_down over FOUR classes of experts by number mod 4 (moe_gemm_q_mod4's): class q at [N_q, "
+      "K_q], expert e at entry e/4 of class e%4; otherwise moe_exl3_down. docs/OPS-exl3.md." },
     { "moe_exl3_prep_gu_mod4", p_pg4, N_OF(p_pg4), o_pg4, N_OF(o_pg4),
-      "moe_exl3_prep_gu over four classes of experts by number mod 4; topk_ids (optional) is a hint only." },
+      "moe_exl3_prep_gu over FOUR classes of experts by number mod 4: class q's input width K_q, expert e "
+      "at entry e/4 of class e%4; xr f16 [T, 2*max(K_q)]; otherwise moe_exl3_prep_gu. topk_ids (optional, "
+      "i32 [M, top_k]): the router's expert of each (token, slot), the sort's input -- a speed hint only, "
+      "the output does not depend on it. docs/OPS-exl3.md." },
     { "moe_exl3_gate_up_down_mod4", p_gd4, N_OF(p_gd4), o_gd4, N_OF(o_gd4),
-      "moe_exl3_gate_up_down over four classes of experts by number mod 4." },
+      "moe_exl3_gate_up_down over FOUR classes of experts by number mod 4: y = moe_exl3_down_mod4(h_rot = "
+      "1) of moe_exl3_gate_up_mod4(a_rot = 0, h_rot = 1) of a; class q at [N_q, K_q], expert e at entry e/4"
+      " of class e%4; otherwise moe_exl3_gate_up_down. docs/OPS-exl3.md." },
 };
 
 /* schema i -> (exl3c4 op, four classes?) */

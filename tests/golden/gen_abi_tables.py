@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Writes exl3_abi_tables.json: the reference's op schemas (parameter specs, operand lists) and operand positions, read
+"""Writes exl3_abi_tables.json: the reference's op schemas (parameter specs, operand lists, doc strings) and operand positions, read
 AS TEXT from /root/reference/include/exl3_abi.h (lines 286-355 positions, 366-627 schemas). Nothing of the reference is
 compiled or imported; the JSON is data the plugin tests compare libexl3c4.so's exports with.
 
@@ -73,11 +73,26 @@ names = {m.group(1): m.group(2) for m in re.finditer(r'#define\s+(EXL3_OP_\w+)\s
 schema_ops = [names[x] for x in listed]
 assert schema_ops == [o for o, _, _ in order], schema_ops
 
+# each schema's doc string: the adjacent string literals of its entry, joined as the C compiler joins them
+docs = []
+depth, start = 0, None
+for j, ch in enumerate(s_body):
+    if ch == "{":
+        depth += 1
+        if depth == 1:
+            start = j
+    elif ch == "}":
+        depth -= 1
+        if depth == 0:
+            docs.append("".join(re.findall(r'"((?:[^"\\]|\\.)*)"', s_body[start:j + 1])))
+assert len(docs) == len(order), len(docs)
+
 schemas = []
-for op, p, o in order:
+for (op, p, o), doc in zip(order, docs):
     schemas.append({"op": op,
                     "params": [[k, kind.replace("RAD_P_", ""), req.replace("RAD_", "")] for k, kind, req in params[p]],
-                    "operands": [[n, d.replace("RAD_OPD_", ""), int(opt)] for n, d, opt in opds[o]]})
+                    "operands": [[n, d.replace("RAD_OPD_", ""), int(opt)] for n, d, opt in opds[o]],
+                    "doc": doc})
 
 pos = {}
 for var, op in (("gu", "moe_exl3_gate_up"), ("dn", "moe_exl3_down"), ("pg", "moe_exl3_prep_gu"),

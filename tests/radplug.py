@@ -163,7 +163,7 @@ def schema_of(lib, i):
                "REQUIRED" if s.params[j].required else "OPTIONAL"] for j in range(s.n_params)]
     opds = [[s.operands[j].name.decode(), {OPD_IN: "IN", OPD_OUT: "OUT", OPD_WTAB: "WTAB"}[s.operands[j].dir],
              int(s.operands[j].optional)] for j in range(s.n_operands)]
-    return {"op": s.op.decode(), "params": params, "operands": opds}
+    return {"op": s.op.decode(), "params": params, "operands": opds, "doc": s.doc.decode()}
 
 
 def shape(row, params, operand):

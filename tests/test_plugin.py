@@ -31,7 +31,8 @@ def test_identity(lib):
 
 
 def test_schemas_are_the_references(lib):
-    """Op names, parameter specs (key, kind, required) and operand lists (name, direction, optional) in order."""
+    """Op names, parameter specs (key, kind, required), operand lists (name, direction, optional) in order, and the doc
+    strings (the engine's loader compares whole schemas)."""
     for i, want in enumerate(TABLES["schemas"]):
         got = rp.schema_of(lib, i)
         assert got == want, f"schema {i} ({want['op']}) differs"
