@@ -1501,43 +1501,50 @@ template <int NW> __device__ __forceinline__ void zero_dead_rows(const Exl3c4Lau
     }
 }
 
-// Stage one 128-k block of up to 64 rows of a row-major f16 source into LDS, permuted (perm_slot) so that each A
-// operand is one ds_read_b128: thread t takes two 16-groups; a group's first 8 halves (k 0..7) land in dwords 0,2,4,6 of
-// the group's 8 stored dwords and its last 8 (k 8..15) in dwords 1,3,5,7. Rows past `nrows` (>= 1) load and store a
-// copy of the last row: every thread issues the same loads, so the waits the compiler counts for the loads issued
-// before them (the codes in flight) stay exact instead of draining; those rows' products are never written.
 // The staged input of one 64-k step of a chunk of R = 16 NT rows: R rows x 4 groups of 16 halves, a group two 16-byte
 // loads, spread over 256 threads (H = ceil(R / 64) groups a thread; a slot past the R x 4 groups reloads the last one,
-// so that the loads stay unconditional and their waits exact). Rows past the chunk load a copy of its last row.
-template <int NT> struct StageRegs { u32x4_t v[2 * ((NT + 3) / 4)]; };
+// so that the loads stay unconditional and their waits exact). Rows past the chunk load a copy of its last row. A
+// slot's address is the step's base (wave-uniform: scalar registers) plus the slot's byte offset, fixed for the chunk
+// and held in a register (32 bits: 2 q pitch + 48 < 2^32 for the q < 96 rows of a chunk, which the host's choice of
+// the prefill path keeps), so the steps' loads take no address arithmetic. The groups land in LDS in row order, k in
+// order: pf_step pairs the decoded B registers to match.
+template <int NT> struct StageRegs {
+    static constexpr int H = (NT + 3) / 4;                        // slots a thread
+    u32x4_t v[2 * H];
+    uint32_t off[H];                                              // each slot's byte offset from the step's base
+};
 template <int NT>
-__device__ __forceinline__ void stage_load(const uint16_t* src, int64_t pitch, int row0, int nrows, int col0,
-                                           StageRegs<NT>& r, int tid) {
-    constexpr int H = (NT + 3) / 4, G = 64 * NT;                  // slots a thread, groups a step
+__device__ __forceinline__ void stage_init(int64_t pitch, int nrows, StageRegs<NT>& r, int tid) {
+    constexpr int G = 64 * NT;                                    // groups a step
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
+    for (int h = 0; h < StageRegs<NT>::H; ++h) {
         const int g = min(tid + 256 * h, G - 1);
-        const int q = min(g >> 2, nrows - 1), grp = g & 3;
+        const uint32_t q = (uint32_t)min(g >> 2, nrows - 1), grp = (uint32_t)(g & 3);
+        r.off[h] = (q * (uint32_t)pitch + grp * 16u) * 2u;
+    }
+}
+// base: the step's first staged column of the chunk's first row, wave-uniform
+template <int NT> __device__ __forceinline__ void stage_load(const uint16_t* base, StageRegs<NT>& r) {
+#pragma unroll
+    for (int h = 0; h < StageRegs<NT>::H; ++h) {
         const __attribute__((address_space(1))) u32x4_t* p = (const __attribute__((address_space(1))) u32x4_t*)
-            (src + (int64_t)(row0 + q) * pitch + col0 + grp * 16);
+            ((const __attribute__((address_space(1))) char*)base + (uint64_t)r.off[h]);
         r.v[2 * h] = p[0];
         r.v[2 * h + 1] = p[1];
     }
 }
-// ... and its store into a step buffer [R][kp], each 16-group permuted (kPerm) so that one 16-byte read is the A
-// operand of two MFMAs.
+// ... and its store into a step buffer [R][kp]
 template <int NT>
 __device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs<NT>& r, int tid) {
-    constexpr int H = (NT + 3) / 4, G = 64 * NT;
+    constexpr int G = 64 * NT;
 #pragma unroll
-    for (int h = 0; h < H; ++h) {
+    for (int h = 0; h < StageRegs<NT>::H; ++h) {
         const int g = tid + 256 * h;
         if (g >= G) break;                                        // uniform in a wave (G is a multiple of 64)
         const int q = g >> 2, grp = g & 3;
-        const u32x4_t lo = r.v[2 * h], hi = r.v[2 * h + 1];
         u32x4_t* d = (u32x4_t*)(A + q * kp + grp * 16);
-        d[0] = u32x4_t{ lo.x, hi.x, lo.y, hi.y };
-        d[1] = u32x4_t{ lo.z, hi.z, lo.w, hi.w };
+        d[0] = r.v[2 * h];
+        d[1] = r.v[2 * h + 1];
     }
 }
 
@@ -1567,8 +1574,11 @@ __device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, const int32
 constexpr int PF_NT = EXL3C4_PF_ROWS / 16;                      // a chunk's row tiles at most
 template <int BITS, int CB, int NT>
 __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[PF_NT][2]) {
-    const half8_t b0 = as_half8(B[0], B[1], B[2], B[3]), b1 = as_half8(B[8], B[9], B[10], B[11]);
-    const half8_t b2 = as_half8(B[4], B[5], B[6], B[7]), b3 = as_half8(B[12], B[13], B[14], B[15]);
+    // the segment's B[j] holds the k pair 2 j' of the lane's 16-group for j' = (0, 4, 1, 5, 2, 6, 3, 7)[j & 7] (the
+    // trellis segment's run order); the staged group is in k order, so Aa (k 0..7) pairs with B[0, 2, 4, 6] and
+    // Ac (k 8..15) with B[1, 3, 5, 7] (and the second 16 columns' with B[8..15] alike)
+    const half8_t b0 = as_half8(B[0], B[2], B[4], B[6]), b1 = as_half8(B[8], B[10], B[12], B[14]);
+    const half8_t b2 = as_half8(B[1], B[3], B[5], B[7]), b3 = as_half8(B[9], B[11], B[13], B[15]);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const uint16_t* arow = Ab + t * 16 * kp;
@@ -1598,8 +1608,9 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
     constexpr int kp = PF_KP;
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = float4_t{ 0.f, 0.f, 0.f, 0.f };   // the chunk's tiles only
-    const int tid = (int)threadIdx.x & 255, sh = NH == 2 ? (int)threadIdx.x >> 8 : 0;  // staged and read half
-    const int scol = col_off + sh * half_off;                     // this thread's staged input column
+    const int tid = (int)threadIdx.x & 255;
+    const int sh = NH == 2 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8) : 0;   // staged and read half
+    const uint16_t* sbase = src + (int64_t)row0 * pitch + col_off + sh * half_off;   // wave-uniform
     auto bufp = [&](int b, int h) { return lds + (b * NH + h) * EXL3C4_PF_ROWS * kp; };
     const gu32p rec = (gu32p)tab_entry(codes, codes_s, jx) + (int64_t)strip * ksteps * 64 * BITS + lane * BITS;
     // the codes of the steps ahead: dA even steps, dB odd; each refill 2 steps ahead of the step it serves (clamped:
@@ -1608,7 +1619,8 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
     load_words<BITS>(rec, dA);
     load_words<BITS>(rec + 64 * BITS, dB);
     StageRegs<NT> r;
-    stage_load<NT>(src, pitch, row0, nrows, scol, r, tid);
+    stage_init<NT>(pitch, nrows, r, tid);
+    stage_load<NT>(sbase, r);
     const Mul1Consts k = mul1_consts();
     stage_store<NT>(bufp(0, sh), kp, r, tid);
     __syncthreads();
@@ -1619,7 +1631,7 @@ __device__ __forceinline__ void pf_gemm_nt(const void* codes, int32_t codes_s, i
         for (int s2 = 0; s2 < 2; ++s2) {                          // step ks = 2 kb + s2 sits in buffer s2
             const int ks = 2 * kb + s2;
             // the next step, or at the last a harmless reload of it: unconditional, like the codes' refills
-            stage_load<NT>(src, pitch, row0, nrows, scol + min(ks + 1, ksteps - 1) * EXL3C4_KSTEP, r, tid);
+            stage_load<NT>(sbase + min(ks + 1, ksteps - 1) * EXL3C4_KSTEP, r);
             uint32_t B[16];
             decode_segment<BITS, CB>(s2 ? dB : dA, B, k);
             const int nx = min(ks + 2, ksteps - 1);

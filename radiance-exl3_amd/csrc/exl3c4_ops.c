@@ -87,16 +87,21 @@ static int log2i(int v) {
  * the prefill kernels, us a launch, M tokens: M = 17: 99 / 110, 24: 118 / 128, 32: 148 / 149, 48: 187 / 184,
  * 64: 219 / 210, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293. The reference serves M >= 17 by its GEMM rows
  * (kernels/exl3r4d/rows.c:255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the band below the
- * crossover. A function of T and n_expert only (never of the routing). */
+ * crossover. A function of T, n_expert and the op's widths (never of the routing): the prefill GEMMs address a chunk's
+ * staged rows by 32-bit byte offsets (2 x 95 x pitch + 64 < 2^32), so an input pitch past EXL3C4_PF_MAX_PITCH halves
+ * (the caller's x, the rotated input's 2 x cols, h's rows / 2) keeps the decode kernels at any T. */
 #ifndef EXL3C4_PF_MIN_T
 #define EXL3C4_PF_MIN_T 64
 #endif
+#define EXL3C4_PF_MAX_PITCH (1 << 24)
 int64_t exl3c4_prefill_min_rows(int64_t n_expert) {
     const int64_t r = (3 * (n_expert > 0 ? n_expert : 0) + 3) / 4;
     return r > EXL3C4_PF_MIN_T ? r : EXL3C4_PF_MIN_T;
 }
 static int prefill_path(const Exl3c4Op* o, int64_t T) {
-    return o->op != EXL3C4_PREP_GU && T >= exl3c4_prefill_min_rows(o->n_expert);
+    const int64_t pitch = o->x_pitch > 2 * max_cols(o) ? o->x_pitch : 2 * max_cols(o);
+    return o->op != EXL3C4_PREP_GU && T >= exl3c4_prefill_min_rows(o->n_expert) && pitch <= EXL3C4_PF_MAX_PITCH &&
+           max_rows(o) / 2 <= EXL3C4_PF_MAX_PITCH;
 }
 
 /* gate_up_down runs as one kernel at decode from this many sorted rows (the header's EXL3C4_GD_FUSE_MIN_T; a build
