@@ -1201,10 +1201,19 @@ constexpr int PF_TILES = EXL3C4_PF_ROWS / 16;                     // row tiles a
 __device__ __forceinline__ const int32_t* pf_order(const Exl3c4Launch& a, int gemm) {
     return a.plan + EXL3C4_PF_PLAN_HDR + 4 * a.max_chunks + gemm * a.max_chunks;
 }
+// The XCD of a chunk whose cost starts at p_excl, of a GEMM whose chunks cost total: its cost midpoint's eighth,
+// min(7, floor(8 (2 p_excl + cost) / (2 total))), counted as the j = 1..7 with 2 j total <= 8 (2 p_excl + cost)
+// (comparisons, no division).
 __device__ __forceinline__ int pf_xcd_of(int p_excl, int cost, int total) {
-    return min(7, (int)((8ll * (2ll * p_excl + cost)) / (2ll * max(total, 1))));
+    const int64_t m8 = 8ll * (2ll * p_excl + cost), t2 = 2ll * max(total, 1);
+    int x = 0;
+#pragma unroll
+    for (int j = 1; j < 8; ++j) x += m8 >= j * t2 ? 1 : 0;
+    return x;
 }
-template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& a) {
+// The plan for any number of experts: a block of NT experts at a time, the chunk entries written, then read back for
+// the XCD deal, the orders and the rows' owners (a round trip of global memory for each).
+template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launch& a) {
     __shared__ int scan[NT];
     __shared__ int carry_s, tiles_s, cnt_g[8], cnt_d[8];
     __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
@@ -1276,6 +1285,7 @@ template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& 
     __syncthreads();
     if (tid == 0) {
         a.plan[0] = nch;
+        a.plan[EXL3C4_PF_SPAN] = 0;                               // the rows' owners in row_info
         int bg = 0, bd = 0;
         for (int x = 0; x < 8; ++x) {
             a.plan[EXL3C4_PF_XCD_GU + x] = bg;
@@ -1316,6 +1326,227 @@ template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& 
         const int4 en = ent[c];
         for (int r = 0; r < en.z; ++r) a.row_info[2 * (en.y + r)] = en.x;
     }
+}
+// An inclusive prefix sum over a workgroup of NT threads (NT / 64 waves) of (tiles << 32 | chunks) pairs: within each
+// wave by lane shuffles, then the waves' totals through LDS (wsum: NT / 64 entries); total: the workgroup's sum. Two
+// barriers.
+template <int NT> __device__ __forceinline__ int64_t block_scan64(int64_t v, int64_t* wsum, int64_t& total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int64_t t = __shfl_up(v, d);
+        if (lane >= d) v += t;
+    }
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    int64_t pre = 0;
+    total = 0;
+#pragma unroll
+    for (int j = 0; j < NT / 64; ++j) {
+        pre += j < w ? wsum[j] : 0;
+        total += wsum[j];
+    }
+    __syncthreads();                                              // wsum is read before the next scan writes it
+    return v + pre;
+}
+// The plan for up to EPT x NT experts, thread tid taking experts tid, NT + tid, ... through every phase (their runs,
+// first chunks and tile prefixes kept in LDS, each entry written and read by its own thread): one round of loads (the
+// offsets), then scans, LDS counters and stores only -- nothing the workgroup writes to global memory is read back, so
+// no phase waits for its stores. The same plan as plan_generic: chunks in expert order, each expert's run clamped to
+// [0, T) and cut into chunks of at most EXL3C4_PF_ROWS rows (all full but the last), the chunks past max_chunks
+// dropped (their rows' owner -1); each chunk's XCDs from its cost midpoint; each GEMM's order by tiles inside an
+// XCD's range; the rows' owners.
+// The plan for up to EPT x NT experts, thread tid taking experts tid, NT + tid, ... (their clamped runs, first chunks
+// and tile prefixes kept in LDS, each entry written and read by its own thread): one round of loads (the offsets),
+// then scans, LDS counters and stores only -- nothing the workgroup writes to global memory is read back, so no phase
+// waits for its stores. The same plan as plan_generic: chunks in expert order, each expert's run clamped to [0, T) and
+// cut into chunks of at most EXL3C4_PF_ROWS rows (all full but the last), the chunks past max_chunks dropped; each
+// chunk's XCDs from its cost midpoint; each GEMM's order by tiles inside an XCD's range. A thread's chunks of one
+// expert fall into runs of equal (XCD, tiles) -- the XCD grows with the chunk index -- and each run costs one LDS
+// atomic: the counts added when a run ends, a run's slots in the order taken by one atomicAdd of its length. The rows'
+// owners: when the offsets ascend and no chunk is dropped, the held rows are the one span [off[0], off[n_expert])
+// (clamped), recorded in the plan's header (EXL3C4_PF_SPAN) for zero_dead_rows; otherwise each row's owner in
+// row_info, as plan_generic writes it.
+template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c4Launch& a) {
+    __shared__ int64_t wsum[NT / 64];
+    __shared__ int cnt_g[8], cnt_d[8], tk_s, desc_s;
+    __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
+    __shared__ int s_lo[EPT * NT], s_hi[EPT * NT], s_first[EPT * NT], s_tf[EPT * NT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
+    if (tid == 0) tk_s = desc_s = 0;
+    if (tid < 8 * PF_TILES) cur_g[tid / PF_TILES][tid % PF_TILES] = cur_d[tid / PF_TILES][tid % PF_TILES] = 0;
+    int lo[EPT], hi[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {                               // the offsets: one round of loads
+        const int e = k * NT + tid;
+        lo[k] = e < a.n_expert ? a.off[e] : 0;
+        hi[k] = e < a.n_expert ? a.off[e + 1] : 0;
+    }
+    int64_t carry = 0;
+    bool desc = false;                                            // an offset below the one before it
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        if (k * NT >= a.n_expert) break;                          // uniform
+        const int e = k * NT + tid;
+        desc = desc || (e < a.n_expert && hi[k] < lo[k]);
+        const int l = min(max(lo[k], 0), a.T), h = min(max(hi[k], l), a.T);
+        const int n = e < a.n_expert ? (h - l + EXL3C4_PF_ROWS - 1) / EXL3C4_PF_ROWS : 0;
+        const int rem = h - l - (n - 1) * EXL3C4_PF_ROWS;        // the last chunk's rows
+        const int tiles = n ? (n - 1) * PF_TILES + ((rem + 15) >> 4) : 0;
+        const int64_t v = ((int64_t)tiles << 32) | (uint32_t)n;
+        int64_t blk;
+        const int64_t ex = carry + block_scan64<NT>(v, wsum, blk) - v;
+        s_lo[e] = l;
+        s_hi[e] = h;
+        s_first[e] = (int)(ex & 0xFFFFFFFF);
+        s_tf[e] = (int)(ex >> 32);                                // tiles of the chunks before this expert's
+        carry += blk;
+    }
+    if (desc) desc_s = 1;
+    const int nch_all = (int)(carry & 0xFFFFFFFF), nch = min(nch_all, a.max_chunks);
+    // the kept chunks' tiles: all of them unless chunks were dropped (those come last in chunk order)
+    int tiles_kept = (int)(carry >> 32);
+    if (nch < nch_all) {                                          // uniform
+        int t = 0;
+#pragma unroll 1
+        for (int k = 0; k < EPT; ++k) {
+            const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e];
+            for (int r0 = l, at = f; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at)
+                t += (min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4;
+        }
+        if (t) atomicAdd(&tk_s, t);
+        __syncthreads();
+        tiles_kept = tk_s;
+    }
+    const int tot_g = EXL3C4_PF_W_GU * nch + tiles_kept, tot_d = EXL3C4_PF_W_DN * nch + tiles_kept;
+    // each chunk's entry {e, first row, rows, XCD of gate_up | XCD of down << 8}; the (XCD, tiles) counts a run at a
+    // time (run: consecutive chunks of the thread's expert of one class, kg / kd = XCD x PF_TILES + tiles - 1)
+    int4* ent = (int4*)(a.plan + EXL3C4_PF_PLAN_HDR);
+#pragma unroll 1
+    for (int k = 0; k < EPT; ++k) {
+        if (k * NT >= a.n_expert) break;                          // uniform
+        const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
+        int kg = -1, kd = -1, ng = 0, nd = 0;
+        for (int r0 = l, at = f, p = tf; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES) {
+            const int rows = min(EXL3C4_PF_ROWS, h - r0), t = (rows + 15) >> 4;   // earlier chunks: full
+            const int xg = pf_xcd_of(EXL3C4_PF_W_GU * at + p, EXL3C4_PF_W_GU + t, tot_g);
+            const int xd = pf_xcd_of(EXL3C4_PF_W_DN * at + p, EXL3C4_PF_W_DN + t, tot_d);
+            ent[at] = make_int4(e, r0, rows, xg | (xd << 8));
+            const int cg = xg * PF_TILES + t - 1, cd = xd * PF_TILES + t - 1;
+            if (cg != kg) {
+                if (ng) {
+                    atomicAdd(&cur_g[0][0] + kg, ng);
+                    atomicAdd(&cnt_g[kg / PF_TILES], ng);
+                }
+                kg = cg;
+                ng = 0;
+            }
+            if (cd != kd) {
+                if (nd) {
+                    atomicAdd(&cur_d[0][0] + kd, nd);
+                    atomicAdd(&cnt_d[kd / PF_TILES], nd);
+                }
+                kd = cd;
+                nd = 0;
+            }
+            ++ng;
+            ++nd;
+        }
+        if (ng) {
+            atomicAdd(&cur_g[0][0] + kg, ng);
+            atomicAdd(&cnt_g[kg / PF_TILES], ng);
+        }
+        if (nd) {
+            atomicAdd(&cur_d[0][0] + kd, nd);
+            atomicAdd(&cnt_d[kd / PF_TILES], nd);
+        }
+    }
+    __syncthreads();
+    const bool span = desc_s == 0 && nch == nch_all;              // the held rows: one span
+    if (tid == 0) {
+        a.plan[0] = nch;
+        a.plan[EXL3C4_PF_SPAN] = span ? 1 : 0;
+        a.plan[EXL3C4_PF_SPAN + 1] = min(max(a.off[0], 0), a.T);
+        a.plan[EXL3C4_PF_SPAN + 2] = min(max(a.off[a.n_expert], 0), a.T);
+        int bg = 0, bd = 0;
+        for (int x = 0; x < 8; ++x) {
+            a.plan[EXL3C4_PF_XCD_GU + x] = bg;
+            a.plan[EXL3C4_PF_XCD_DN + x] = bd;
+            bg += cnt_g[x];
+            bd += cnt_d[x];
+        }
+        a.plan[EXL3C4_PF_XCD_GU + 8] = bg;
+        a.plan[EXL3C4_PF_XCD_DN + 8] = bd;
+    }
+    // each GEMM's order: inside an XCD's range, chunks of more row tiles first (the longest units start first, so
+    // the range ends on short ones); chunks of equal tiles in any order (where a unit runs changes no bits)
+    if (tid < 16) {
+        int (*cur)[PF_TILES] = tid < 8 ? cur_g : cur_d;
+        const int x = tid & 7;
+        int at = 0;
+        for (int y = 0; y < x; ++y) at += (tid < 8 ? cnt_g : cnt_d)[y];
+        for (int k = PF_TILES - 1; k >= 0; --k) {
+            const int c = cur[x][k];
+            cur[x][k] = at;
+            at += c;
+        }
+    }
+    __syncthreads();
+    int32_t* ord_g = (int32_t*)(ent + a.max_chunks);
+    int32_t* ord_d = ord_g + a.max_chunks;
+    // a run's slots: one atomicAdd of its length when it ends, then its chunks (consecutive indices) in them
+    auto place = [&](int32_t* ord, int* cur, int key, int n, int at_end) {
+        const int base = atomicAdd(cur + key, n);
+        for (int j = 0; j < n; ++j) ord[base + j] = at_end - n + j;
+    };
+#pragma unroll 1
+    for (int k = 0; k < EPT; ++k) {
+        if (k * NT >= a.n_expert) break;                          // uniform
+        const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
+        int kg = -1, kd = -1, ng = 0, nd = 0, at = f;
+        for (int r0 = l, p = tf; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES) {
+            const int t = (min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4;
+            const int cg = pf_xcd_of(EXL3C4_PF_W_GU * at + p, EXL3C4_PF_W_GU + t, tot_g) * PF_TILES + t - 1;
+            const int cd = pf_xcd_of(EXL3C4_PF_W_DN * at + p, EXL3C4_PF_W_DN + t, tot_d) * PF_TILES + t - 1;
+            if (cg != kg) {
+                if (ng) place(ord_g, &cur_g[0][0], kg, ng, at);
+                kg = cg;
+                ng = 0;
+            }
+            if (cd != kd) {
+                if (nd) place(ord_d, &cur_d[0][0], kd, nd, at);
+                kd = cd;
+                nd = 0;
+            }
+            ++ng;
+            ++nd;
+        }
+        if (ng) place(ord_g, &cur_g[0][0], kg, ng, at);
+        if (nd) place(ord_d, &cur_d[0][0], kd, nd, at);
+    }
+    if (span) return;                                             // uniform
+    // each row's owner (row_info[i] = {e or -1, 0}): every row -1, then, once those stores have completed, the rows
+    // of the kept chunks' runs their expert, written by the wave's lanes side by side one expert at a time (a row two
+    // runs hold, from offsets that do not ascend, takes either expert)
+    for (int i = tid; i < a.T; i += NT) *(int2*)(a.row_info + 2 * i) = make_int2(-1, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+#pragma unroll 1
+    for (int k = 0; k < EPT; ++k) {
+        const int e0 = k * NT + 64 * wave;
+        if (e0 >= a.n_expert) break;                              // uniform
+        const int ml = s_lo[e0 + lane];                           // the wave's 64 experts, lane-parallel
+        const int mh = min(s_hi[e0 + lane], ml + max(0, nch - s_first[e0 + lane]) * EXL3C4_PF_ROWS);   // past it:
+        for (int j = 0; j < 64; ++j) {                                                                // dropped
+            const int l = __builtin_amdgcn_readlane(ml, j), hk = __builtin_amdgcn_readlane(mh, j);   // chunks' rows,
+            for (int r = l + lane; r < hk; r += 64) a.row_info[2 * r] = e0 + j;                      // left -1
+        }
+    }
+}
+template <int NT> __device__ __forceinline__ void plan_body(const Exl3c4Launch& a) {
+    if (a.n_expert <= 4 * NT) plan_fast<NT, 4>(a);
+    else plan_generic<NT>(a);
 }
 __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) { plan_body<1024>(a); }
 
@@ -1374,14 +1605,17 @@ __device__ __forceinline__ void load8w(const uint16_t* p, bool wide, uint32_t (&
     }
 }
 
-// The rotation into scratch, one wave per sorted row, 8 consecutive elements a lane: a pass covers 4 128-blocks of
-// each half (one 16-byte load of x, one of each scale and one store a half a lane), and the loads of up to ROT_PASSES
-// passes go out together: gate_up's xr (halves 0 and 1 from the same token row: suh, suh1 of the row's expert) or
-// down's rotated h (one half: down's suh, sorted rows in). The first step f16(x su) is one f16 multiply (v_pk_mul_f16:
-// the exact product rounded once, as f16(f32(x) f32(su)) rounds it; bf16 x: in f32, then rounded). The rows are dealt
-// to the XCDs in contiguous ranges, so a run's rows (one expert's scales) share an L2. Rows no run holds are not
-// written (nothing reads them); a negative sorted_tok gives zeros.
-constexpr int ROT_PASSES = 2;
+// The rotation into scratch, ROT_ROWS consecutive sorted rows a wave, 8 consecutive elements a lane: a pass covers 4
+// 128-blocks of each half of each row (one 16-byte load of x, one of each scale and one store a half a lane), and the
+// loads of up to ROT_PASSES passes of all the wave's rows go out together: gate_up's xr (halves 0 and 1 from the same
+// token row: suh, suh1 of the row's expert) or down's rotated h (one half: down's suh, sorted rows in). A row's chain
+// (its owner, its class's tables, its loads, then the stores) is a few dependent round trips that the write stream
+// lengthens; a wave runs its rows' chains side by side, and the stores are non-temporal (xr is read once, by the
+// GEMM, after the 4 MiB L2s have turned over). The first step f16(x su) is one f16 multiply (v_pk_mul_f16: the exact
+// product rounded once, as f16(f32(x) f32(su)) rounds it; bf16 x: in f32, then rounded). The rows are dealt to the
+// XCDs in contiguous ranges, so a run's rows (one expert's scales) share an L2. Rows no run holds are not written
+// (nothing reads them); a negative sorted_tok gives zeros.
+constexpr int ROT_PASSES = 2, ROT_ROWS = 2;
 // f32 (lo of w) + f32 (hi of w) and f32 (lo) - f32 (hi) of a dword of two f16 values: each one v_fma_mix_f32 (the f16
 // sources taken exactly, one rounding), the first butterfly stage of two neighbours straight from their packed f16
 // product -- as the f16 -> f32 conversions then an f32 add and subtract would round them.
@@ -1391,109 +1625,202 @@ __device__ __forceinline__ void mix_sum_diff(uint32_t w, float& sum, float& dif)
         : "=&v"(sum), "=v"(dif) : "v"(w));
 }
 
-// One row's passes: per pass each lane's 8 consecutive columns of each half (BF: x in bf16), as described at k_rot.
-template <bool BF, int HALVES>
-__device__ __forceinline__ void rot_passes(const uint16_t* x, const uint16_t* s0, const uint16_t* s1, uint16_t* out,
-                                           int C, int npass, int lcol, int g, bool xw, bool sw, const RotSigns& ks) {
+// One wave's R rows of one class (C columns): per pass each lane's 8 consecutive columns of each half of each row
+// (BF: x in bf16), as described at k_rot. Row r: x[r] its input row, s0[r] / s1[r] its expert's scales, out[r] its xr
+// row; zero[r]: written as zeros (a negative sorted_tok; its loads read a valid row, unused); wr[r]: written at all.
+template <bool BF, int HALVES, int R>
+__device__ __forceinline__ void rot_passes(const uint16_t* const (&x)[R], const uint16_t* const (&s0)[R],
+                                           const uint16_t* const (&s1)[R], uint16_t* const (&out)[R],
+                                           const bool (&zero)[R], const bool (&wr)[R], int C, int npass, int lcol,
+                                           int g, bool xw, bool sw, const RotSigns& ks) {
     for (int p0 = 0; p0 < npass; p0 += ROT_PASSES) {
-        uint32_t xq[ROT_PASSES][4], sq[2][ROT_PASSES][4];
+        uint32_t xq[R][ROT_PASSES][4], sq[R][2][ROT_PASSES][4];
 #pragma unroll
-        for (int q = 0; q < ROT_PASSES; ++q) {
-            int col = (p0 + q) * 512 + lcol;
-            col = col < C ? col : 8 * g;                            // past the row: reload the first block (unused)
-            load8w(x + col, xw, xq[q]);
-            load8w(s0 + col, sw, sq[0][q]);
-            if (HALVES == 2) load8w(s1 + col, sw, sq[1][q]);
-        }
-#pragma unroll
-        for (int m = 0; m < HALVES; ++m) {
+        for (int r = 0; r < R; ++r)
 #pragma unroll
             for (int q = 0; q < ROT_PASSES; ++q) {
-                if (p0 + q >= npass) break;
-                float v[8];
-                if (BF) {
+                int col = (p0 + q) * 512 + lcol;
+                col = col < C ? col : 8 * g;                        // past the row: reload the first block (unused)
+                load8w(x[r] + col, xw, xq[r][q]);
+                load8w(s0[r] + col, sw, sq[r][0][q]);
+                if (HALVES == 2) load8w(s1[r] + col, sw, sq[r][1][q]);
+            }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (!wr[r]) continue;                                 // uniform
+#pragma unroll
+            for (int m = 0; m < HALVES; ++m) {
+#pragma unroll
+                for (int q = 0; q < ROT_PASSES; ++q) {
+                    if (p0 + q >= npass) break;
+                    float v[8];
+                    if (BF) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const uint32_t xb = xq[r][q][j], sb = sq[r][m][q][j];
+                            v[2 * j] = h2f(f2h(bf2f((uint16_t)xb) * h2f((uint16_t)sb)));
+                            v[2 * j + 1] = h2f(f2h(bf2f((uint16_t)(xb >> 16)) * h2f((uint16_t)(sb >> 16))));
+                        }
+                        had128_x8(v, ks);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const half2_t pr = __builtin_bit_cast(half2_t, xq[r][q][j]) *
+                                               __builtin_bit_cast(half2_t, sq[r][m][q][j]);
+                            mix_sum_diff(__builtin_bit_cast(uint32_t, pr), v[2 * j], v[2 * j + 1]);   // stage h = 1
+                        }
+                        had128_x8<2>(v, ks);
+                    }
+                    u32x4_t o;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const uint32_t xb = xq[q][j], sb = sq[m][q][j];
-                        v[2 * j] = h2f(f2h(bf2f((uint16_t)xb) * h2f((uint16_t)sb)));
-                        v[2 * j + 1] = h2f(f2h(bf2f((uint16_t)(xb >> 16)) * h2f((uint16_t)(sb >> 16))));
+                        typedef float float2v __attribute__((ext_vector_type(2)));
+                        const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
+                        o[j] = zero[r] ? 0u : __builtin_bit_cast(uint32_t, hv);
                     }
-                    had128_x8(v, ks);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const half2_t pr = __builtin_bit_cast(half2_t, xq[q][j]) * __builtin_bit_cast(half2_t, sq[m][q][j]);
-                        mix_sum_diff(__builtin_bit_cast(uint32_t, pr), v[2 * j], v[2 * j + 1]);   // stage h = 1
-                    }
-                    had128_x8<2>(v, ks);
+                    const int col = (p0 + q) * 512 + lcol;
+                    if (col < C) __builtin_nontemporal_store(o, (u32x4_t*)(out[r] + m * C + col));
                 }
-                uint32_t o[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    typedef float float2v __attribute__((ext_vector_type(2)));
-                    const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
-                    o[j] = __builtin_bit_cast(uint32_t, hv);
-                }
-                const int col = (p0 + q) * 512 + lcol;
-                if (col < C) *(uint4*)(out + m * C + col) = uint4{ o[0], o[1], o[2], o[3] };
             }
         }
     }
 }
+
+// The owners of the R sorted rows i0 .. i0 + R - 1 (-1: no run holds the row, or it lies past T): owner_wave's
+// search, its one round of loads shared by the rows (off[] read once, a ballot count a row).
+template <int R>
+__device__ __forceinline__ void owner_rows(const int32_t* off, int n_expert, int i0, int T, int lane, int (&e)[R]) {
+    constexpr int OJ = 9;
+    if (n_expert < 64 * OJ) {
+        int o[OJ];
+#pragma unroll
+        for (int j = 0; j < OJ; ++j) o[j] = off[min(lane + 64 * j, n_expert)];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = i0 + r;
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < OJ; ++j) {
+                const int ej = lane + 64 * j;
+                cnt += __popcll(__ballot(ej >= 1 && ej <= n_expert && o[j] <= i));
+            }
+            const int er = min(cnt, n_expert - 1);
+            int lo = 0, hi = 0;
+#pragma unroll
+            for (int j = 0; j < OJ; ++j) {
+                if ((er >> 6) == j) lo = __builtin_amdgcn_readlane(o[j], er & 63);
+                if (((er + 1) >> 6) == j) hi = __builtin_amdgcn_readlane(o[j], (er + 1) & 63);
+            }
+            e[r] = (i < T && lo <= i && i < hi) ? er : -1;
+        }
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        e[r] = i0 + r < T ? __builtin_amdgcn_readfirstlane(owner_wave(off, n_expert, i0 + r, lane)) : -1;
+}
+
+template <bool BF, int HALVES>
+__device__ __forceinline__ void rot_rows(const Exl3c4Launch& a, int i0, const int (&e)[ROT_ROWS],
+                                         const int (&tok)[ROT_ROWS], int lane) {
+    // the rows' class: one class for all held rows (the usual case) runs them side by side, else one at a time
+    int eb = -1;
+#pragma unroll
+    for (int r = ROT_ROWS - 1; r >= 0; --r) eb = e[r] >= 0 ? e[r] : eb;
+    if (eb < 0) return;                                           // no row held
+    bool same = true;
+#pragma unroll
+    for (int r = 0; r < ROT_ROWS; ++r) same = same && (e[r] < 0 || class_of(a, e[r]) == class_of(a, eb));
+    const int g = rot_group(lane & 15), lcol = 128 * (lane >> 4) + 8 * g;   // the lane's columns in a pass
+    const RotSigns ks = rot_signs(g);
+    const bool xw = (((uintptr_t)a.x | (uintptr_t)(a.x_pitch * 2)) & 15) == 0;
+    auto row = [&](int r, const Exl3c4DevClass& K, const uint16_t*& x, const uint16_t*& s0, const uint16_t*& s1,
+                   uint16_t*& out, bool& zero, bool& wr) {
+        const int er = e[r] >= 0 ? e[r] : eb, i = i0 + r;
+        const int64_t jx = entry_of(a, er);
+        int64_t src = HALVES == 2 ? (tok[r] < 0 ? 0 : tok[r] / a.top_k) : min(i, a.T - 1);
+        src = src < a.x_rows ? src : a.x_rows - 1;
+        x = (const uint16_t*)a.x + src * a.x_pitch;
+        s0 = (const uint16_t*)tab_entry(K.suh, K.suh_s, jx);
+        s1 = HALVES == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_s, jx) : s0;
+        out = (uint16_t*)a.y + (int64_t)min(i, a.T - 1) * a.y_pitch;
+        zero = tok[r] < 0;
+        wr = e[r] >= 0;
+    };
+    if (same) {
+        const Exl3c4DevClass& K = a.cls[class_of(a, eb)];
+        const uint16_t* x[ROT_ROWS];
+        const uint16_t* s0[ROT_ROWS];
+        const uint16_t* s1[ROT_ROWS];
+        uint16_t* out[ROT_ROWS];
+        bool zero[ROT_ROWS], wr[ROT_ROWS];
+        bool sw = true;
+#pragma unroll
+        for (int r = 0; r < ROT_ROWS; ++r) {
+            row(r, K, x[r], s0[r], s1[r], out[r], zero[r], wr[r]);
+            sw = sw && ((((uintptr_t)s0[r] | (uintptr_t)s1[r]) & 15) == 0);
+        }
+        const int C = K.cols, npass = (C / 128 + 3) / 4;
+        rot_passes<BF, HALVES, ROT_ROWS>(x, s0, s1, out, zero, wr, C, npass, lcol, g, xw, sw, ks);
+        return;
+    }
+#pragma unroll 1
+    for (int r = 0; r < ROT_ROWS; ++r) {
+        if (e[r] < 0) continue;
+        const Exl3c4DevClass& K = a.cls[class_of(a, e[r])];
+        const uint16_t* x[1];
+        const uint16_t* s0[1];
+        const uint16_t* s1[1];
+        uint16_t* out[1];
+        bool zero[1], wr[1];
+        row(r, K, x[0], s0[0], s1[0], out[0], zero[0], wr[0]);
+        const bool sw = (((uintptr_t)s0[0] | (uintptr_t)s1[0]) & 15) == 0;
+        const int C = K.cols, npass = (C / 128 + 3) / 4;
+        rot_passes<BF, HALVES, 1>(x, s0, s1, out, zero, wr, C, npass, lcol, g, xw, sw, ks);
+    }
+}
+
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     if (a.plan && blockIdx.x == 0) {                              // the launch's first workgroup plans the GEMMs
+        // at the top wave priority: the plan's short chain of phases would otherwise get a few of the issue slots
+        // of the rows' VALU-bound waves on its CU
+        __builtin_amdgcn_s_setprio(3);
         plan_body<256>(a);
         return;
     }
     const int lane = threadIdx.x & 63;
     const int gb = (int)blockIdx.x - (a.plan ? 1 : 0);
-    const int nwg = (a.T + 3) / 4, per_xcd = (nwg + 7) / 8;
+    const int nwg = (a.T + 4 * ROT_ROWS - 1) / (4 * ROT_ROWS), per_xcd = (nwg + 7) / 8;
     const int wg = (gb & 7) * per_xcd + (gb >> 3);
-    // the row, its owner and its sorted_tok taken wave-uniform: the class descriptor and the row's entries are then
-    // scalar loads that go out together, not vector loads each waited for
-    const int i = __builtin_amdgcn_readfirstlane(wg * 4 + (int)(threadIdx.x >> 6));
-    if (wg >= nwg || i >= a.T) return;
-    const int halves = a.h_from_gu;                             // here: 2 for gate_up's xr, 1 for down's h
-    const int tok_v = a.sorted[i];                                // out with the owner search's loads
-    const int e = __builtin_amdgcn_readfirstlane(owner_wave(a.off, a.n_expert, i, lane));   // the plan writes row_info
-    const int tok = __builtin_amdgcn_readfirstlane(tok_v);       // uniform: the row's addresses are scalar
-    if (e < 0) return;
-    const Exl3c4DevClass& K = a.cls[class_of(a, e)];
-    const int64_t jx = entry_of(a, e);
-    const int C = K.cols;
-    uint16_t* out = (uint16_t*)a.y + (int64_t)i * a.y_pitch;
-    const int npass = (C / 128 + 3) / 4;
-    const int g = rot_group(lane & 15), lcol = 128 * (lane >> 4) + 8 * g;   // the lane's columns in a pass
-    if (tok < 0) {
-        for (int p = 0; p < npass * halves; ++p) {
-            const int col = (p % npass) * 512 + lcol;
-            if (col < C) *(uint4*)(out + (p / npass) * C + col) = uint4{ 0, 0, 0, 0 };
-        }
-        return;
-    }
-    const RotSigns ks = rot_signs(g);
-    int64_t src = halves == 2 ? tok / a.top_k : i;
-    src = src < a.x_rows ? src : a.x_rows - 1;
-    const uint16_t* x = (const uint16_t*)a.x + src * a.x_pitch;
-    const uint16_t* s0 = (const uint16_t*)tab_entry(K.suh, K.suh_s, jx);
-    const uint16_t* s1 = halves == 2 ? (const uint16_t*)tab_entry(K.suh1, K.suh1_s, jx) : s0;
-    const bool xw = (((uintptr_t)a.x | (uintptr_t)(a.x_pitch * 2)) & 15) == 0;
-    const bool sw = (((uintptr_t)s0 | (uintptr_t)s1) & 15) == 0;
-    if (halves == 2) {
-        if (a.x_dtype == EXL3C4_BF16) rot_passes<true, 2>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
-        else rot_passes<false, 2>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
+    // the rows, their owners and their sorted_tok taken wave-uniform: the class descriptor and the rows' entries are
+    // then scalar loads that go out together, not vector loads each waited for
+    const int i0 = __builtin_amdgcn_readfirstlane((wg * 4 + (int)(threadIdx.x >> 6)) * ROT_ROWS);
+    if (wg >= nwg || i0 >= a.T) return;
+    const int tok_v = a.sorted[min(i0 + (lane & (ROT_ROWS - 1)), a.T - 1)];   // lane r: row i0 + r's, out with the
+    int e[ROT_ROWS], tok[ROT_ROWS];                                             // owner search's loads
+    owner_rows<ROT_ROWS>(a.off, a.n_expert, i0, a.T, lane, e);   // the plan writes row_info
+#pragma unroll
+    for (int r = 0; r < ROT_ROWS; ++r) tok[r] = __builtin_amdgcn_readlane(tok_v, r);
+    if (a.h_from_gu == 2) {                                       // here: 2 halves for gate_up's xr, 1 for down's h
+        if (a.x_dtype == EXL3C4_BF16) rot_rows<true, 2>(a, i0, e, tok, lane);
+        else rot_rows<false, 2>(a, i0, e, tok, lane);
     } else {
-        rot_passes<false, 1>(x, s0, s1, out, C, npass, lcol, g, xw, sw, ks);
+        rot_rows<false, 1>(a, i0, e, tok, lane);
     }
 }
 
 // Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows): wave w of
 // workgroup z takes row z * NW + w (NW: the kernel's waves a workgroup): the workgroups from a.tail_from of the last
-// GEMM's launch.
+// GEMM's launch. The held rows: the plan's span, or where it records none, the rows' owners in row_info.
 template <int NW> __device__ __forceinline__ void zero_dead_rows(const Exl3c4Launch& a, int z) {
     const int lane = threadIdx.x & 63;
     const int64_t i = (int64_t)z * NW + (threadIdx.x >> 6);
-    if (i >= a.T || a.row_info[2 * i] >= 0) return;
+    if (i >= a.T) return;
+    if (a.plan[EXL3C4_PF_SPAN]) {                                 // the held rows: one span, from the plan's header
+        if (i >= a.plan[EXL3C4_PF_SPAN + 1] && i < a.plan[EXL3C4_PF_SPAN + 2]) return;
+    } else if (a.row_info[2 * i] >= 0) {
+        return;
+    }
     uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
     for (int b = 0; b < a.nblk; ++b) {
         out[b * 128 + lane] = 0;
@@ -2114,7 +2441,7 @@ extern "C" int exl3c4_dev_plan(const Exl3c4Launch* a, void* stream, void* ev0, v
 
 extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     if (a->T <= 0) return 0;
-    const unsigned nwg = (unsigned)((a->T + 3) / 4);
+    const unsigned nwg = (unsigned)((a->T + 4 * ROT_ROWS - 1) / (4 * ROT_ROWS));
     return go(k_rot, 8 * ((nwg + 7) / 8) + (a->plan ? 1 : 0), (hipStream_t)stream, ev0, ev1, *a);
 }
 

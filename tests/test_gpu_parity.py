@@ -169,6 +169,40 @@ def test_owner_search_on_both_sides_of_its_one_round_form(torch_cuda, n_expert):
     _check_all(case, f"owner search, {n_expert} experts")
 
 
+def test_prefill_plan_with_offsets_that_do_not_ascend(torch_cuda):
+    """The plan's other record of the held rows. Offsets [100, 20, 50, 120, 160] over 4 experts (160 sorted rows):
+    expert 0's run [100, max(20, 100)) is empty, experts 1-3 hold [20, 50), [50, 120), [120, 160) once each, and no
+    run holds [0, 20). The held rows are then no single span from off[0], so the plan writes each row's owner and the
+    dead-row zeroing reads it (ascending offsets take the span instead). y equals the oracle's chain on the same
+    offsets (kernels/exl3r4d/launch.c:14-15 clamps the runs alike), the rows no run holds are zero, and a replay
+    writes the same bits."""
+    import exl3c4
+    from gpuchecks import chain_ok
+    case = Case(seed=91, n_tok=40, top_k=4, n_expert=4, geoms=[(256, 128)], bits=4, cb="mul1")
+    assert case.T == 160 and exl3c4.is_prefill(case.T, case.n_expert)
+    case.off = np.array([100, 20, 50, 120, 160], dtype=case.off.dtype)
+    _say("prefill plan, offsets that do not ascend")
+    dev = Dev(case)
+    gd = dev.gate_up_down()
+    assert chain_ok("gate_up_down", bf16(gd), bf16(case.oracle_gate_up_down()))
+    dead = np.array([i < 20 or case.sorted_tok[i] < 0 for i in range(case.T)])
+    assert dead[:20].all() and not dead.all()
+    assert np.all(gd[dead] == 0)
+    assert np.any(gd[~dead] != 0)
+    assert np.array_equal(dev.gate_up_down(), gd)
+    dev.check_tables()
+
+
+def test_prefill_plan_past_its_register_form(torch_cuda):
+    """1040 experts: past the 4 x 256 experts the rotation launch's planning workgroup holds in its threads, so the
+    plan takes its general form (blocks of 256 experts, the entries read back); 800 sorted rows, every op against
+    the oracle."""
+    import exl3c4
+    case = Case(seed=93, n_tok=200, top_k=4, n_expert=1040, geoms=[(256, 128)], bits=4, cb="mul1", drop=0.05)
+    assert exl3c4.is_prefill(case.T, case.n_expert)
+    _check_all(case, "prefill 1040 experts")
+
+
 def test_prefill_path_bf16_3inst(torch_cuda):
     _check_all(Case(seed=42, n_tok=64, top_k=1, n_expert=2, geoms=[(256, 128)], bits=3, cb="3inst", x_bf16=True),
                "prefill bf16")
