@@ -68,6 +68,14 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// Two f32 VALUES -> f16 (lo in the low half), each rounded to nearest even: one v_cvt_pk_f16_f32 (gfx950), the
+// operands materialised as f2h's are.
+__device__ __forceinline__ uint32_t f2h2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){ lo, hi }, f16x2_t));
+}
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 // Two f32 to bf16 (lo in the low half): round to nearest even on the f32 bits, a nan kept quiet as (u >> 16) | 0x40
 // (radiance's rad_f32_to_bf16). One v_cvt_pk_bf16_f32 (gfx950), which gives those bits for every f32: compared on
@@ -1671,8 +1679,8 @@ __device__ __forceinline__ void rot_passes(const uint16_t* const (&x)[R], const 
                         }
                         had128_x8<2>(v, ks);
                     }
-                    u32x4_t o;
-#pragma unroll
+                    u32x4_t o;                                    // (a v_cvt_pk_f16_f32 of the scaled values:
+#pragma unroll                                                    // the bits are checked against prep_gu's)
                     for (int j = 0; j < 4; ++j) {
                         typedef float float2v __attribute__((ext_vector_type(2)));
                         const half2_t hv = __builtin_convertvector(float2v{ v[2 * j], v[2 * j + 1] }, half2_t);
@@ -2051,6 +2059,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             sd[0] = sd[1] = sd[2] = sd[3] = 0;
         }
     }
+    float sgf[8], suf[8];                                         // the gate and up scales as f32, once
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        sgf[j] = h2f((uint16_t)(sg[j >> 1] >> (16 * (j & 1))));
+        suf[j] = h2f((uint16_t)(su[j >> 1] >> (16 * (j & 1))));
+    }
     const bool yw = ((((uintptr_t)a.y) | ((uintptr_t)a.y_pitch * 2)) & 15) == 0;
     float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
 #pragma unroll
@@ -2085,24 +2099,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             const int tk = row < 64 ? tk_lo : tk_hi;
             had128_x8(gv, ks);
             had128_x8(uv, ks);
-            uint16_t hv[8];
+            uint32_t o[4];                                        // h, two f16 values a dword
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float gs = gv[j] * h2f((uint16_t)(sg[j >> 1] >> (16 * (j & 1))));
-                const float us = uv[j] * h2f((uint16_t)(su[j >> 1] >> (16 * (j & 1))));
-                hv[j] = f2h(silu(gs) * us);
+            for (int j = 0; j < 4; ++j) {
+                const float h0 = silu(gv[2 * j] * sgf[2 * j]) * (uv[2 * j] * suf[2 * j]);
+                const float h1 = silu(gv[2 * j + 1] * sgf[2 * j + 1]) * (uv[2 * j + 1] * suf[2 * j + 1]);
+                o[j] = f2h2(h0, h1);
             }
             if (a.h_rot) {
+                // f16(h dn_suh): one f16 multiply of the pair (the exact product rounded once, as f16(f32 f32) rounds
+                // it), its first butterfly stage straight from the packed product (mix_sum_diff), then the rest
                 float rv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) rv[j] = h2f(f2h(h2f(hv[j]) * h2f((uint16_t)(sd[j >> 1] >> (16 * (j & 1))))));
-                had128_x8(rv, ks);
+                for (int j = 0; j < 4; ++j) {
+                    const half2_t pr = __builtin_bit_cast(half2_t, o[j]) * __builtin_bit_cast(half2_t, sd[j]);
+                    mix_sum_diff(__builtin_bit_cast(uint32_t, pr), rv[2 * j], rv[2 * j + 1]);
+                }
+                had128_x8<2>(rv, ks);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) hv[j] = f2h(rv[j]);
+                for (int j = 0; j < 4; ++j) o[j] = f2h2(rv[2 * j], rv[2 * j + 1]);
             }
-            uint32_t o[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = tk < 0 ? 0u : ((uint32_t)hv[2 * j] | ((uint32_t)hv[2 * j + 1] << 16));
+            for (int j = 0; j < 4; ++j) o[j] = tk < 0 ? 0u : o[j];
             if (row < rend) {
                 uint16_t* out = (uint16_t*)a.y + (int64_t)(row0 + row) * a.y_pitch + gcol;
                 if (yw) {
