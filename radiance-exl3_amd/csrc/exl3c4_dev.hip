@@ -1616,14 +1616,14 @@ __device__ __forceinline__ void load8w(const uint16_t* p, bool wide, uint32_t (&
 // The rotation into scratch, ROT_ROWS consecutive sorted rows a wave, 8 consecutive elements a lane: a pass covers 4
 // 128-blocks of each half of each row (one 16-byte load of x, one of each scale and one store a half a lane), and the
 // loads of up to ROT_PASSES passes of all the wave's rows go out together: gate_up's xr (halves 0 and 1 from the same
-// token row: suh, suh1 of the row's expert) or down's rotated h (one half: down's suh, sorted rows in). A row's chain
-// (its owner, its class's tables, its loads, then the stores) is a few dependent round trips that the write stream
-// lengthens; a wave runs its rows' chains side by side, and the stores are non-temporal (xr is read once, by the
-// GEMM, after the 4 MiB L2s have turned over). The first step f16(x su) is one f16 multiply (v_pk_mul_f16: the exact
+// token row: suh, suh1 of the row's expert) or down's rotated h (one half: down's suh, sorted rows in). A wave can run
+// several rows' chains (owner, class tables, loads, stores) side by side; one row a wave measured fastest (2048
+// tokens: 45.2 us against 46.9 for two rows and 54.2 for four: more rows a wave cost resident waves). The stores are
+// non-temporal (xr is read once, by the GEMM, after the 4 MiB L2s have turned over). The first step f16(x su) is one f16 multiply (v_pk_mul_f16: the exact
 // product rounded once, as f16(f32(x) f32(su)) rounds it; bf16 x: in f32, then rounded). The rows are dealt to the
 // XCDs in contiguous ranges, so a run's rows (one expert's scales) share an L2. Rows no run holds are not written
 // (nothing reads them); a negative sorted_tok gives zeros.
-constexpr int ROT_PASSES = 2, ROT_ROWS = 2;
+constexpr int ROT_PASSES = 2, ROT_ROWS = 1;
 // f32 (lo of w) + f32 (hi of w) and f32 (lo) - f32 (hi) of a dword of two f16 values: each one v_fma_mix_f32 (the f16
 // sources taken exactly, one rounding), the first butterfly stage of two neighbours straight from their packed f16
 // product -- as the f16 -> f32 conversions then an f32 add and subtract would round them.
