@@ -1817,22 +1817,22 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     }
 }
 
-// Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows): wave w of
-// workgroup z takes row z * NW + w (NW: the kernel's waves a workgroup): the workgroups from a.tail_from of the last
-// GEMM's launch. The held rows: the plan's span, or where it records none, the rows' owners in row_info.
+// Zero the 128-blocks of y of the rows no run holds (the prefill GEMMs write only their chunks' rows): the
+// PF_TAIL_WG workgroups from a.tail_from of the last GEMM's launch, wave w of workgroup z taking rows z * NW + w,
+// then every PF_TAIL_WG * NW rows on (NW: the kernel's waves a workgroup). The held rows: the plan's span, or where it
+// records none, the rows' owners in row_info.
+constexpr int PF_TAIL_WG = 256;
 template <int NW> __device__ __forceinline__ void zero_dead_rows(const Exl3c4Launch& a, int z) {
     const int lane = threadIdx.x & 63;
-    const int64_t i = (int64_t)z * NW + (threadIdx.x >> 6);
-    if (i >= a.T) return;
-    if (a.plan[EXL3C4_PF_SPAN]) {                                 // the held rows: one span, from the plan's header
-        if (i >= a.plan[EXL3C4_PF_SPAN + 1] && i < a.plan[EXL3C4_PF_SPAN + 2]) return;
-    } else if (a.row_info[2 * i] >= 0) {
-        return;
-    }
-    uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
-    for (int b = 0; b < a.nblk; ++b) {
-        out[b * 128 + lane] = 0;
-        out[b * 128 + lane + 64] = 0;
+    const bool span = a.plan[EXL3C4_PF_SPAN] != 0;
+    const int lo = a.plan[EXL3C4_PF_SPAN + 1], hi = a.plan[EXL3C4_PF_SPAN + 2];
+    for (int64_t i = (int64_t)z * NW + (threadIdx.x >> 6); i < a.T; i += (int64_t)PF_TAIL_WG * NW) {
+        if (span ? (i >= lo && i < hi) : a.row_info[2 * i] >= 0) continue;   // held: a chunk writes it
+        uint16_t* out = (uint16_t*)a.y + i * a.y_pitch;
+        for (int b = 0; b < a.nblk; ++b) {
+            out[b * 128 + lane] = 0;
+            out[b * 128 + lane + 64] = 0;
+        }
     }
 }
 
@@ -2473,8 +2473,8 @@ extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     if (a->n_grp < 2 || a->max_chunks <= 0) return 0;
     Exl3c4Launch g = *a;
     const int units = 8 * (a->n_grp / 2) * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_GU);
-    g.tail_from = a->tail_from ? units : 0;                       // then (T + 7) / 8 workgroups zero dead rows
-    const dim3 grid((unsigned)(units + (g.tail_from ? (a->T + 7) / 8 : 0)));
+    g.tail_from = a->tail_from ? units : 0;                       // then PF_TAIL_WG workgroups zero dead rows
+    const dim3 grid((unsigned)(units + (g.tail_from ? PF_TAIL_WG : 0)));
     if (ev0 && ev1)
         hipExtLaunchKernelGGL(f, grid, dim3(512), 0, (hipStream_t)stream, (hipEvent_t)ev0, (hipEvent_t)ev1, 0, g);
     else
@@ -2488,8 +2488,8 @@ extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
     Exl3c4Launch g = *a;
     const int units = 8 * a->nblk * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_DN);
-    g.tail_from = a->tail_from ? units : 0;                       // then (T + 3) / 4 workgroups zero dead rows
-    return go2(f, dim3((unsigned)(units + (g.tail_from ? (a->T + 3) / 4 : 0))), (hipStream_t)stream, ev0, ev1, 0u, g);
+    g.tail_from = a->tail_from ? units : 0;                       // then PF_TAIL_WG workgroups zero dead rows
+    return go2(f, dim3((unsigned)(units + (g.tail_from ? PF_TAIL_WG : 0))), (hipStream_t)stream, ev0, ev1, 0u, g);
 }
 
 extern "C" int exl3c4_dev_dequant(const void* record, int32_t rows, int32_t cols, int32_t bits, int32_t codebook,
