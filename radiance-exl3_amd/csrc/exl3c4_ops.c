@@ -84,10 +84,11 @@ static int log2i(int v) {
  * 4 T >= 3 n_expert (exl3c4_prefill_min_rows). Below it the decode kernels serve it (chunks of up to 16 rows, split-K;
  * gate_up_down as one kernel from EXL3C4_GD_FUSE_MIN_T rows). The rule is the crossover measured on MI355X at the
  * decode layer's experts (512 experts, 2048 / 512, K = 4, softmax top-10): gate_up_down by the decode kernels against
- * the prefill kernels, us a launch, M tokens: M = 17: 99 / 110, 24: 118 / 128, 32: 148 / 149, 48: 187 / 184,
- * 64: 219 / 210, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293. The reference serves M >= 17 by its GEMM rows
- * (kernels/exl3r4d/rows.c:255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the band below the
- * crossover. A function of T, n_expert and the op's widths (never of the routing): the prefill GEMMs address a chunk's
+ * the prefill kernels, us a launch, M tokens: M = 17: 82 / 99, 24: 108 / 117, 32: 135 / 135, 40: 153 / 155,
+ * 48: 172 / 163, 64: 204 / 191 (and, measured on an earlier build, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293):
+ * the rule's M >= 39 (T >= 384) sits in the band where the two differ by under 2%. The reference serves M >= 17 by
+ * its GEMM rows (kernels/exl3r4d/rows.c:255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the
+ * band below the crossover. A function of T, n_expert and the op's widths (never of the routing): the prefill GEMMs address a chunk's
  * staged rows by 32-bit byte offsets (2 x 95 x pitch + 64 < 2^32), so an input pitch past EXL3C4_PF_MAX_PITCH halves
  * (the caller's x, the rotated input's 2 x cols, h's rows / 2) keeps the decode kernels at any T. */
 #ifndef EXL3C4_PF_MIN_T
