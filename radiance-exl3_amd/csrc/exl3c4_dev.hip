@@ -1790,9 +1790,6 @@ __device__ __forceinline__ void rot_rows(const Exl3c4Launch& a, int i0, const in
 
 __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     if (a.plan && blockIdx.x == 0) {                              // the launch's first workgroup plans the GEMMs
-        // at the top wave priority: the plan's short chain of phases would otherwise get a few of the issue slots
-        // of the rows' VALU-bound waves on its CU
-        __builtin_amdgcn_s_setprio(3);
         plan_body<256>(a);
         return;
     }
@@ -1806,7 +1803,7 @@ __global__ __launch_bounds__(256) void k_rot(const Exl3c4Launch a) {
     if (wg >= nwg || i0 >= a.T) return;
     const int tok_v = a.sorted[min(i0 + (lane & (ROT_ROWS - 1)), a.T - 1)];   // lane r: row i0 + r's, out with the
     int e[ROT_ROWS], tok[ROT_ROWS];                                             // owner search's loads
-    owner_rows<ROT_ROWS>(a.off, a.n_expert, i0, a.T, lane, e);   // the plan writes row_info
+    owner_rows<ROT_ROWS>(a.off, a.n_expert, i0, a.T, lane, e);   // -1: a row no run holds, not written
 #pragma unroll
     for (int r = 0; r < ROT_ROWS; ++r) tok[r] = __builtin_amdgcn_readlane(tok_v, r);
     if (a.h_from_gu == 2) {                                       // here: 2 halves for gate_up's xr, 1 for down's h
