@@ -146,3 +146,22 @@ def test_an_accepted_op_reaches_the_scratch_check():
         o = op(which, E=4)
         assert exl3c4.lib().exl3c4_launch(C.byref(o), None, 0, None) == -20
     assert Fake((2, 3)).numel() == 6
+
+
+def test_input_pitches_past_the_prefill_offsets_keep_the_decode_kernels():
+    """The prefill GEMMs address a chunk's staged rows by 32-bit byte offsets from a wave-uniform base, so the prefill
+    path takes input pitches up to 2^24 halves; past that a launch of any T runs on the decode kernels, and its
+    scratch is theirs (the split-K partial sums), not the prefill path's (the plan, the rotated input)."""
+    T = 96 * 10
+    assert exl3c4.is_prefill(T, 512)
+
+    def sized(pitch):
+        o = op(exl3c4.GU_DN, H=2048, W=512, E=512, M=96, top_k=10)
+        o.x_pitch = pitch
+        return exl3c4.launch_scratch_bytes(o)
+
+    at, past = sized(1 << 24), sized((1 << 24) + 64)
+    assert sized(2048) == at                     # within the bound: the prefill path, whatever the pitch
+    assert past > 0 and past != at
+    small = op(exl3c4.GU_DN, H=2048, W=512, E=512, M=96, top_k=10, rows_T=T)
+    assert exl3c4.launch_scratch_bytes(small) == at
