@@ -101,16 +101,21 @@ __device__ __forceinline__ int had_col_t(int lane) {
 
 // The normalised Sylvester Hadamard over one 128-block held by a wave: the butterfly stages h = 1 .. 64 in the
 // reference's order, each (a + b) low and (a - b) high in f32, then one f32 multiply by 1/sqrt(128)
-// (common/exl3_decode.c:172-189) -- the same roundings, so the same bits. Bits 0..3 of an element sit in bits 0..3 of
+// (common/exl3_decode.c:172-189) -- the same roundings, so the same values. Bits 0..3 of an element sit in bits 0..3 of
 // its lane (had_col); bits 4, 5 and 6 in lane bit 4, lane bit 5 and the register (v0, v1), in an order each stage
 // from h = 16 on changes. For h = 1, 2, 4, 8 the stage is one v_fmac_f32 whose partner operand comes by DPP:
 // v += c p with c = -1 where bit h of the element is set, which leaves those lanes the NEGATED result
 // (v - p = -(p - v)); a partner's element has the same lower bits, hence the same sign, so c needs no correction,
 // and the signs are undone by the final multiply (by -1/sqrt(128) where an odd number of the bits 1, 2, 4, 8 of the
-// element are set). For h = 16, 32, 64 one permlane swap of v0 and v1 (gfx950: VDST's odd 16-lane rows with
-// SRC0's even rows, or VDST's upper 32 lanes with SRC0's lower ones) brings the stage's bit from the lane into the
-// register, so the pair sits in one lane and the stage is an add and a subtract; the bit the register held goes to
-// the lane. The DPP and swap stages run with the whole wave active: every caller's branch around them is uniform.
+// element are set). Negation is exact, so every nonzero result is the reference's bits; an exact zero is not
+// negated by the trick (v - p = +0 where v = p, whose negation would be -0), so the final step is
+// fma(v, +-1/sqrt(128), +0), which gives every zero output +0. That is the reference's zero wherever any of the
+// block's 128 inputs is nonzero (values not all zero that cancel sum to +0 in round-to-nearest, and a stage makes -0
+// only from two zero operands); a block of 128 zeros rotates to +0 throughout, where the reference's exact-sign
+// stages can leave -0 at some outputs (the same value, the other sign bit). For h = 16, 32, 64 one permlane swap of
+// v0 and v1 (gfx950: VDST's odd 16-lane rows with SRC0's even rows, or VDST's upper 32 lanes with SRC0's lower ones)
+// brings the stage's bit from the lane into the register, so the pair sits in one lane and the stage is an add and a
+// subtract; the bit the register held goes to the lane. The DPP and swap stages run with the whole wave active: every caller's branch around them is uniform.
 #define HAD_DPP(v, c, CTRL) asm volatile("s_nop 1\n\tv_fmac_f32_dpp %0, %0, %1 " CTRL " row_mask:0xf bank_mask:0xf" \
                                          : "+v"(v) : "v"(c))
 // v0 and v1 exchanged across 16-lane rows (W = 16) or 32-lane halves (W = 32): a lane of the odd row (upper half)
@@ -157,8 +162,8 @@ template <bool T_IN> __device__ __forceinline__ void had128_wave(float& v0, floa
     a = v0 + v1;
     b = v0 - v1;
     const float sc = (__builtin_popcount(j & 15) & 1) ? -kHadScale : kHadScale;
-    v0 = a * sc;
-    v1 = b * sc;
+    v0 = __builtin_fmaf(a, sc, 0.f);                              // + 0: an exact zero leaves as +0 (see HAD_DPP)
+    v1 = __builtin_fmaf(b, sc, 0.f);
 }
 
 // The expert owning sorted row i -- e with off[e] <= i < off[e + 1], or -1 (include/exl3_abi.h:136-141) -- found
@@ -1223,10 +1228,13 @@ __device__ __forceinline__ int pf_xcd_of(int p_excl, int cost, int total) {
 // the XCD deal, the orders and the rows' owners (a round trip of global memory for each).
 template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launch& a) {
     __shared__ int scan[NT];
-    __shared__ int carry_s, tiles_s, cnt_g[8], cnt_d[8];
+    __shared__ int carry_s, tiles_s, cut_s, cnt_g[8], cnt_d[8];
     __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
     const int tid = threadIdx.x;
-    if (tid == 0) carry_s = tiles_s = 0;
+    if (tid == 0) {
+        carry_s = tiles_s = 0;
+        cut_s = 0x7FFFFFFF;
+    }
     if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
     if (tid < 8 * PF_TILES) cur_g[tid / PF_TILES][tid % PF_TILES] = cur_d[tid / PF_TILES][tid % PF_TILES] = 0;
     __syncthreads();
@@ -1262,9 +1270,40 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
         if (tid == NT - 1) carry_s += scan[NT - 1];
         __syncthreads();
     }
-    const int nch = min(carry_s, a.max_chunks);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // the entries, read by other threads below
+    __syncthreads();
+    int nch = min(carry_s, a.max_chunks);
+    // the tile budget, T / 16 + min(n_expert, T) (the launch's grid holds the chunks of at most that many tiles, with
+    // max_chunks; runs that do not overlap never pass it): the chunks from the first whose running tiles pass it are
+    // dropped, as those past max_chunks are
+    const int budget = a.T / 16 + min(a.n_expert, a.T);
+    if (tiles_s > budget) {                                       // uniform
+        int run = 0;
+        for (int base = 0; base < nch; base += NT) {
+            const int c = base + tid;
+            const int t = c < nch ? (ent[c].z + 15) >> 4 : 0;
+            scan[tid] = t;
+            __syncthreads();
+            for (int d = 1; d < NT; d <<= 1) {
+                const int u = tid >= d ? scan[tid - d] : 0;
+                __syncthreads();
+                scan[tid] += u;
+                __syncthreads();
+            }
+            if (c < nch && run + scan[tid] > budget) atomicMin(&cut_s, c);
+            run += scan[NT - 1];
+            __syncthreads();
+        }
+        if (tid == 0) tiles_s = 0;
+        __syncthreads();
+        nch = min(nch, cut_s);
+        int t = 0;                                                // the kept chunks' tiles
+        for (int c = tid; c < nch; c += NT) t += (ent[c].z + 15) >> 4;
+        if (t) atomicAdd(&tiles_s, t);
+        __syncthreads();
+    }
     const int tot_g = EXL3C4_PF_W_GU * nch + tiles_s, tot_d = EXL3C4_PF_W_DN * nch + tiles_s;
-    // the chunks' tile prefix (this workgroup wrote the entries: visible after the barrier above)
+    // the chunks' tile prefix
     int carry = 0;
     for (int base = 0; base < nch; base += NT) {
         const int c = base + tid;
@@ -1290,6 +1329,7 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
         carry += scan[NT - 1];
         __syncthreads();
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // the entries' XCDs, read by other threads below
     __syncthreads();
     if (tid == 0) {
         a.plan[0] = nch;
@@ -1377,12 +1417,15 @@ template <int NT> __device__ __forceinline__ int64_t block_scan64(int64_t v, int
 // row_info, as plan_generic writes it.
 template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c4Launch& a) {
     __shared__ int64_t wsum[NT / 64];
-    __shared__ int cnt_g[8], cnt_d[8], tk_s, desc_s;
+    __shared__ int cnt_g[8], cnt_d[8], tk_s, desc_s, cut_s;
     __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
     __shared__ int s_lo[EPT * NT], s_hi[EPT * NT], s_first[EPT * NT], s_tf[EPT * NT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
-    if (tid == 0) tk_s = desc_s = 0;
+    if (tid == 0) {
+        tk_s = desc_s = 0;
+        cut_s = 0x7FFFFFFF;
+    }
     if (tid < 8 * PF_TILES) cur_g[tid / PF_TILES][tid % PF_TILES] = cur_d[tid / PF_TILES][tid % PF_TILES] = 0;
     int lo[EPT], hi[EPT];
 #pragma unroll
@@ -1412,7 +1455,25 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
         carry += blk;
     }
     if (desc) desc_s = 1;
-    const int nch_all = (int)(carry & 0xFFFFFFFF), nch = min(nch_all, a.max_chunks);
+    // the tile budget, T / 16 + min(n_expert, T) (the launch's grid holds the chunks of at most that many tiles, with
+    // max_chunks; runs that do not overlap never pass it): the chunks from the first whose running tiles pass it are
+    // dropped, as those past max_chunks are -- found by the one expert whose chunks cross it
+    const int budget = a.T / 16 + min(a.n_expert, a.T);
+    if ((int)(carry >> 32) > budget) {                            // uniform
+#pragma unroll 1
+        for (int k = 0; k < EPT; ++k) {
+            const int e = k * NT + tid;
+            if (e >= a.n_expert) break;
+            const int l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
+            for (int r0 = l, at = f, p = tf; r0 < h; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES)
+                if (p + ((min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4) > budget) {
+                    atomicMin(&cut_s, at);
+                    break;
+                }
+        }
+        __syncthreads();
+    }
+    const int nch_all = (int)(carry & 0xFFFFFFFF), nch = min(min(nch_all, a.max_chunks), cut_s);
     // the kept chunks' tiles: all of them unless chunks were dropped (those come last in chunk order)
     int tiles_kept = (int)(carry >> 32);
     if (nch < nch_all) {                                          // uniform
@@ -1565,8 +1626,10 @@ __global__ __launch_bounds__(1024) void k_plan(const Exl3c4Launch a) { plan_body
 // h = 8, 16, 32, 64 (bits 0 .. 3 of g) pair lane l with l ^ 1, l ^ 2, l ^ 7, l ^ 8 -- the lanes whose g differs in that
 // bit alone, each one DPP move (quad_perm, quad_perm, row_half_mirror, row_ror 8) -- as in had128_wave: v_fmac by
 // c = -1 on the lanes whose g has the stage's bit set leaves them the NEGATED result, the partner (same lower bits of
-// g) carries the same sign, and the final multiply by -1/sqrt(128) where popcount(g) is odd undoes it. The reference's
-// stages in its order with its roundings (common/exl3_decode.c:172-189), so the same bits.
+// g) carries the same sign, and the final multiply by -1/sqrt(128) where popcount(g) is odd undoes it, as an fma with
+// +0 (an exact zero leaves as +0, as had128_wave's does). The reference's stages in its order with its roundings
+// (common/exl3_decode.c:172-189), so the same values, and the same bits but for the sign of zeros that had128_wave
+// states.
 __device__ __forceinline__ int rot_group(int l) { return l ^ (((l >> 2) & 1) * 3); }
 #define HAD_DPP8_OP(I, CTRL) "v_fmac_f32_dpp %" #I ", %" #I ", %8 " CTRL " row_mask:0xf bank_mask:0xf\n\t"
 // one stage over the 8 values: a lane's v[j] was written 8 moves before it is read, so one s_nop (the DPP read-after-
@@ -1599,7 +1662,7 @@ __device__ __forceinline__ void had128_x8(float (&v)[8], const RotSigns& k) {
     HAD_DPP8(v, k.c4, "row_half_mirror");
     HAD_DPP8(v, k.c8, "row_ror:8");
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = v[j] * k.sc;
+    for (int j = 0; j < 8; ++j) v[j] = __builtin_fmaf(v[j], k.sc, 0.f);   // + 0: an exact zero leaves as +0
 }
 
 // 8 consecutive halves at p as 4 dwords (16-byte aligned: one load; else eight)
@@ -2460,16 +2523,22 @@ extern "C" int exl3c4_dev_rot(const Exl3c4Launch* a, void* stream, void* ev0, vo
     return go(k_rot, 8 * ((nwg + 7) / 8) + (a->plan ? 1 : 0), (hipStream_t)stream, ev0, ev1, *a);
 }
 
-// The most chunks k_plan can deal one XCD: the midpoints of its chunks lie in a stretch of total / 8 (total <=
-// (W + 4) chunks) and are at least W + 1 apart.
-static int pf_xcd_bound(int max_chunks, int w) { return (int)(((int64_t)(w + 4) * max_chunks) / (8 * (w + 1))) + 2; }
+// The most chunks the plan can deal one XCD: the cost midpoints of its chunks lie in a stretch of total / 8 and are
+// at least W + 1 apart (each chunk costs W + tiles >= W + 1), so it holds at most total / (8 (W + 1)) + 1 of them;
+// total = W x chunks + their tiles <= W max_chunks + pf_tile_budget (the plan keeps no chunk past either).
+static int64_t pf_tile_budget(const Exl3c4Launch* a) {
+    return (int64_t)a->T / 16 + (a->n_expert < a->T ? a->n_expert : a->T);
+}
+static int pf_xcd_bound(const Exl3c4Launch* a, int w) {
+    return (int)(((int64_t)w * a->max_chunks + pf_tile_budget(a)) / (8 * (w + 1))) + 2;
+}
 
 extern "C" int exl3c4_dev_gu_pf(const Exl3c4Launch* a, void* stream, void* ev0, void* ev1) {
     const GemmFn f = by_bits<GuPfK>(a->bits, a->codebook);
     if (!f) return EXL3C4_E_DTYPE;
     if (a->n_grp < 2 || a->max_chunks <= 0) return 0;
     Exl3c4Launch g = *a;
-    const int units = 8 * (a->n_grp / 2) * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_GU);
+    const int units = 8 * (a->n_grp / 2) * pf_xcd_bound(a, EXL3C4_PF_W_GU);
     g.tail_from = a->tail_from ? units : 0;                       // then PF_TAIL_WG workgroups zero dead rows
     const dim3 grid((unsigned)(units + (g.tail_from ? PF_TAIL_WG : 0)));
     if (ev0 && ev1)
@@ -2484,7 +2553,7 @@ extern "C" int exl3c4_dev_dn_pf(const Exl3c4Launch* a, void* stream, void* ev0, 
     if (!f) return EXL3C4_E_DTYPE;
     if (a->nblk <= 0 || a->max_chunks <= 0) return 0;
     Exl3c4Launch g = *a;
-    const int units = 8 * a->nblk * pf_xcd_bound(a->max_chunks, EXL3C4_PF_W_DN);
+    const int units = 8 * a->nblk * pf_xcd_bound(a, EXL3C4_PF_W_DN);
     g.tail_from = a->tail_from ? units : 0;                       // then PF_TAIL_WG workgroups zero dead rows
     return go2(f, dim3((unsigned)(units + (g.tail_from ? PF_TAIL_WG : 0))), (hipStream_t)stream, ev0, ev1, 0u, g);
 }

@@ -203,6 +203,65 @@ def test_prefill_plan_past_its_register_form(torch_cuda):
     _check_all(case, "prefill 1040 experts")
 
 
+XCD_CROWD = [1] * 26 + [1042, 2577, 1375, 2556]      # rows an expert, top_k 1: 7,576 sorted rows
+
+
+def test_prefill_xcd_ranges_hold_every_chunk_of_a_crowded_range(torch_cuda):
+    """26 one-row experts, then 4 experts of 1,042-2,577 rows (top_k 1): the plan deals down's chunks to the XCDs by
+    cost, and the range of the one-row chunks holds 26 of them, one more than a bound from max_chunks alone gives
+    an XCD (25), whose last chunk's rows of y would go uncomputed. The bound counts the tiles the launch can hold
+    (T / 16 + n_expert, the plan dropping chunks past that budget), and every op of the case meets the oracle."""
+    import exl3c4
+    ids = np.repeat(np.arange(len(XCD_CROWD), dtype=np.int32), XCD_CROWD)
+    ids = np.random.default_rng(95).permutation(ids)[:, None]
+    case = Case(seed=95, n_tok=ids.shape[0], top_k=1, n_expert=len(XCD_CROWD), geoms=[(256, 128)], bits=4,
+                cb="mul1", expert_ids=ids)
+    assert case.T == 7576 and exl3c4.is_prefill(case.T, case.n_expert)
+    _check_all(case, "prefill crowded XCD range")
+
+
+@pytest.mark.parametrize("n_tok,top_k", [(6, 2), (96, 4)])
+def test_rotations_give_exact_zeros_the_reference_sign(torch_cuda, n_tok, top_k):
+    """x of small integers and suh, suh1 of +-1: many rotated values are exact zeros (sums that cancel). The
+    reference's stages are exact-sign a + b, a - b (common/exl3_decode.c:172-189; its device form
+    kernels/exl3r4d/exl3r4d_common.hip.h:178-182 likewise), so such a zero is +0; the device's one-instruction DPP
+    stages leave half the lanes negated and undo it by a final fma with +0, which makes every zero +0: prep_gu's xr
+    equals the oracle's to the bit. Token 0's x is all zeros: its blocks rotate to +0 throughout, where the oracle's
+    butterflies on the signed zeros of x su leave -0 at some outputs -- the same values, the one place the sign bits
+    differ; so do the h_rot rotations of its rows' h (zero too), on the decode path (6 tokens) and the prefill path
+    (96 tokens, 384 sorted rows), while every other row's h_rot output is down's first step on h to the bit."""
+    import exl3c4
+    case = Case(seed=97, n_tok=n_tok, top_k=top_k, n_expert=4, geoms=[(256, 128)], bits=4, cb="mul1")
+    assert exl3c4.is_prefill(case.T, case.n_expert) == (n_tok > 6)
+    rng = np.random.default_rng(98)
+    x = rng.integers(-2, 3, size=(n_tok, 256)).astype(np.float16)
+    x[0] = 0
+    case.x = x.view(np.uint16)
+    for g in case.gu:
+        g.suh = (rng.integers(0, 2, 256) * 2 - 1).astype(np.float16)
+        g.suh1 = (rng.integers(0, 2, 256) * 2 - 1).astype(np.float16)
+    _say(f"rotation zero signs, {n_tok} tokens")
+    dev = Dev(case)
+    xr_d, xr_o = dev.prep(), case.oracle_prep()
+    st = case.sorted_tok
+    held = np.array([case.off[0] <= i < case.off[-1] and st[i] >= 0 for i in range(case.T)])
+    zero_tok = held & (st // top_k == 0)
+    rest = ~zero_tok
+    assert zero_tok.any() and rest.any()
+    assert np.array_equal(xr_d[rest], xr_o[rest]), f"{np.count_nonzero(xr_d[rest] != xr_o[rest])} elements differ"
+    n_zero = int(np.count_nonzero(xr_o[rest & held] == 0))
+    _say(f"  {n_zero} exact +0 outputs among {xr_o[rest & held].size} held values")
+    assert n_zero >= xr_o[rest & held].size // 100
+    assert np.all(xr_d[zero_tok] == 0)                                  # +0 throughout
+    assert np.all(f16(xr_o[zero_tok]) == 0) and np.any(xr_o[zero_tok] == 0x8000)
+
+    h0 = dev.gate_up(h_rot=0)
+    h1, want = dev.gate_up(h_rot=1), case.h_rot_of(h0)
+    assert np.all(f16(h0[zero_tok]) == 0)
+    assert np.array_equal(h1[rest], want[rest])
+    assert np.all(h1[zero_tok] == 0) and np.all(f16(want[zero_tok]) == 0)
+
+
 def test_prefill_path_bf16_3inst(torch_cuda):
     _check_all(Case(seed=42, n_tok=64, top_k=1, n_expert=2, geoms=[(256, 128)], bits=3, cb="3inst", x_bf16=True),
                "prefill bf16")
