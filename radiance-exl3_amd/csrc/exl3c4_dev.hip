@@ -1331,6 +1331,7 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // the entries' XCDs, read by other threads below
     __syncthreads();
+    if (tid < 16) __hip_atomic_store(a.plan + EXL3C4_PF_CUR + 32 * tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         a.plan[0] = nch;
         a.plan[EXL3C4_PF_SPAN] = 0;                               // the rows' owners in row_info
@@ -1533,6 +1534,7 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
     }
     __syncthreads();
     const bool span = desc_s == 0 && nch == nch_all;              // the held rows: one span
+    if (tid < 16) __hip_atomic_store(a.plan + EXL3C4_PF_CUR + 32 * tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         a.plan[0] = nch;
         a.plan[EXL3C4_PF_SPAN] = span ? 1 : 0;
@@ -1944,28 +1946,81 @@ __device__ __forceinline__ void stage_store(uint16_t* A, int kp, const StageRegs
 }
 
 // The prefill GEMMs' workgroups and XCDs: XCD x (the dispatcher deals linear ids g to the XCDs in turn, x = g % 8)
-// takes the plan's contiguous chunk range [xb[x], xb[x + 1]) -- ranges of about equal cost, from k_plan -- its slot
-// g / 8 = per q + u running unit u (0 .. per-1: the chunk's column groups or blocks) of the range's q-th chunk in
-// this GEMM's order (ord: the chunks of more row tiles first, so the range's last units are its shortest). A chunk's
-// units run side by side in one L2, so its staged rows come from HBM once; an expert's chunks fall in one or two
-// ranges, its full chunks side by side in one tile class, so they too share an L2 and, running close in time, read
-// the expert's codes from HBM about once. False for a workgroup with no chunk (the grid covers pf_xcd_bound chunks an
-// XCD). (Where a workgroup lands changes no bits.)
-__device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, const int32_t* ord, int& unit, int& chunk) {
+// takes the plan's contiguous chunk range [xb[x], xb[x + 1]) -- ranges of about equal cost, from k_plan -- as
+// n = per x (its chunks) units in this GEMM's order (ord: the chunks of more row tiles first, so the range's last
+// units are its shortest; unit s: the (s % per)-th running unit -- column group or block -- of the range's (s /
+// per)-th chunk). Slot g / 8 takes unit g / 8 itself, up to the range's last R units; those are dealt by the XCD's
+// cursor (cur + 32 x, zeroed by the plan) to its later slots, and a slot that finds its XCD's cursor spent takes one
+// from the XCD with the most units left (a range's cost is an estimate: the XCDs' ends spread by about half a unit),
+// or returns false when every range is spent. A chunk's units run side by side in one L2, so its staged rows come
+// from HBM once; an expert's chunks fall in one or two ranges, its full chunks side by side in one tile class, so
+// they too share an L2 and, running close in time, read the expert's codes from HBM about once. No workgroup waits;
+// the cursors hand out each unit once, and the grid's pf_xcd_bound chunks' units an XCD cover every range. (Where a
+// workgroup lands changes no bits.)
+template <int R>
+__device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, const int32_t* ord, int32_t* cur, int& unit,
+                                         int& chunk) {
     const int g = (int)blockIdx.x, slot = g >> 3, x = g & 7;
-    const int q = slot / per;
-    unit = slot - q * per;
-    const int at = xb[x] + q;
-    if (at >= xb[x + 1]) return false;
-    chunk = ord[at];
+    const int n = (xb[x + 1] - xb[x]) * per, st = max(n - R, 0);
+    if (slot >= n + R) return false;                              // past the range's end by a round: nothing to take
+    int y = x, s = slot;
+    if (slot >= st) {                                             // the range's last R units, or R slots past its end
+        __shared__ int take_s[2];
+        if (threadIdx.x == 0) {
+            int ty = -1, ts = 0;
+            if (slot < n) {                                       // a slot of the range: its cursor first
+                const int v = st + __hip_atomic_fetch_add(cur + 32 * x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (v < n) {
+                    ty = x;
+                    ts = v;
+                }
+            }
+            // past the range (the first R of the grid's slots beyond it), or its cursor spent: the XCD with the most
+            // units left.
+            // Each failed take finds a range spent that the next search skips, so 8 searches see every range spent.
+            for (int tries = 0; ty < 0 && tries < 8; ++tries) {
+                int best = -1, left = 0, lz[8];
+#pragma unroll
+                for (int z = 0; z < 8; ++z)
+                    lz[z] = __hip_atomic_load(cur + 32 * z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                for (int z = 0; z < 8; ++z) {
+                    const int nz = (xb[z + 1] - xb[z]) * per, rz = nz - max(nz - R, 0) - lz[z];
+                    if (rz > left) {
+                        left = rz;
+                        best = z;
+                    }
+                }
+                if (best < 0) break;
+                const int nb = (xb[best + 1] - xb[best]) * per, sb = max(nb - R, 0);
+                const int v = sb + __hip_atomic_fetch_add(cur + 32 * best, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (v < nb) {
+                    ty = best;
+                    ts = v;
+                }
+            }
+            take_s[0] = ty;
+            take_s[1] = ts;
+        }
+        __syncthreads();
+        y = take_s[0];
+        s = take_s[1];
+        if (y < 0) return false;
+    }
+    const int q = s / per;
+    unit = s - q * per;
+    chunk = ord[xb[y] + q];
     return true;
 }
+// each XCD's units dealt by its cursor: about one round of its slots (gate_up: 2 workgroups a CU x 32 CUs; down: 4)
+constexpr int PF_DYN_GU = 64, PF_DYN_DN = 128;
 
 // One k-step of the prefill GEMM: the step's B operands (decoded just before) against each of the chunk's NT row
 // tiles (4 MFMAs a tile), each group ending in mfma_guard: gfx950 does not interlock a VALU or LDS write against an
-// in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (The SIMD already runs one wave's MFMAs
-// under the other waves' decode -- measured about 75-80% hidden with 4 waves a SIMD -- so a step issued behind the
-// next step's decode gained nothing and cost a second set of B registers.)
+// in-flight 16x16x32 MFMA's A/B reads, and the compiler does not pad for it. (A step's decode and its MFMAs take
+// their sum on a SIMD of 4 such waves, measured: the decode keeps the VALU pipe full and the MFMAs of the other waves
+// find no slot beside it; a step issued behind the next step's decode, or the waves split into a decoding and a
+// multiplying half each half-step, gained nothing.)
 constexpr int PF_NT = EXL3C4_PF_ROWS / 16;                      // a chunk's row tiles at most
 template <int BITS, int CB, int NT>
 __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[PF_NT][2]) {
@@ -2073,7 +2128,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     int hb, chunk;
-    if (!xcd_unit(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, pf_order(a, 0), hb, chunk)) return;
+    if (!xcd_unit<PF_DYN_GU>(a.n_grp / 2, a.plan + EXL3C4_PF_XCD_GU, pf_order(a, 0), a.plan + EXL3C4_PF_CUR, hb,
+                             chunk))
+        return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
@@ -2208,7 +2265,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return;
     }
     int b, chunk;
-    if (!xcd_unit(a.nblk, a.plan + EXL3C4_PF_XCD_DN, pf_order(a, 1), b, chunk)) return;
+    if (!xcd_unit<PF_DYN_DN>(a.nblk, a.plan + EXL3C4_PF_XCD_DN, pf_order(a, 1), a.plan + EXL3C4_PF_CUR + 256, b,
+                             chunk))
+        return;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int4 ent = ((const int4*)(a.plan + EXL3C4_PF_PLAN_HDR))[chunk];
     const int e = __builtin_amdgcn_readfirstlane(ent.x), row0 = __builtin_amdgcn_readfirstlane(ent.y),
