@@ -220,6 +220,20 @@ def test_prefill_xcd_ranges_hold_every_chunk_of_a_crowded_range(torch_cuda):
     _check_all(case, "prefill crowded XCD range")
 
 
+def test_prefill_units_dealt_by_the_xcd_cursors(torch_cuda):
+    """Two experts of 1,900 and 148 rows (top_k 1, 2,048 sorted rows, 22 chunks): each XCD's range holds a few
+    chunks' units, fewer than the round a cursor deals, so every unit of both GEMMs goes out through the XCDs'
+    cursors, and the XCDs whose ranges are spent (or empty) take units from the others. Every op of the case meets
+    the oracle, the rows of y and h equal to the bit across a replay (each unit handed out once, wherever it ran)."""
+    import exl3c4
+    ids = np.array([0] * 1900 + [1] * 148, dtype=np.int32)
+    ids = np.random.default_rng(99).permutation(ids)[:, None]
+    case = Case(seed=99, n_tok=ids.shape[0], top_k=1, n_expert=2, geoms=[(256, 128)], bits=4, cb="mul1",
+                expert_ids=ids)
+    assert case.T == 2048 and exl3c4.is_prefill(case.T, case.n_expert)
+    _check_all(case, "prefill units by cursors")
+
+
 @pytest.mark.parametrize("n_tok,top_k", [(6, 2), (96, 4)])
 def test_rotations_give_exact_zeros_the_reference_sign(torch_cuda, n_tok, top_k):
     """x of small integers and suh, suh1 of +-1: many rotated values are exact zeros (sums that cancel). The
