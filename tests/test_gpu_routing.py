@@ -125,6 +125,33 @@ def test_router_topk_scatter_matches_the_oracle(torch_cuda, n_tok, E, top_k):
         assert np.array_equal(g.cpu().numpy(), w_), name
 
 
+@pytest.mark.parametrize("n_tok,E,top_k,dt", [(8, 512, 10, "f32"), (5, 100, 7, "f16"), (1, 64, 64, "bf16"),
+                                               (9, 512, 10, "f32")])
+def test_router_topk_scatter_routes_to_the_bit_of_the_router(torch_cuda, n_tok, E, top_k, dt):
+    """router_topk_scatter's routing (one workgroup, a wave a token) against router_topk's (a wave a token, four a
+    workgroup) on the same logits: ids and weights to the bit, f32, f16 and bf16 logits, ties included (half-step
+    logits in a row)."""
+    import exl3c4
+    torch = torch_cuda
+    rng = np.random.default_rng(300 + n_tok)
+    lg = rng.standard_normal((n_tok, E)).astype(np.float32)
+    lg[0] = np.round(lg[0] * 2) / 2
+    lg_t = torch.from_numpy(lg).cuda()
+    if dt != "f32":
+        lg_t = lg_t.to(torch.float16 if dt == "f16" else torch.bfloat16)
+    T = n_tok * top_k
+    for renorm in (True, False):
+        ids_r, w_r = _router(torch, lg_t, top_k, renorm)
+        ids = torch.full((n_tok, top_k), -7, dtype=torch.int32, device="cuda")
+        w = torch.full((n_tok, top_k), -7.0, dtype=torch.float32, device="cuda")
+        st = torch.full((T,), -7, dtype=torch.int32, device="cuda")
+        off = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda")
+        assert exl3c4.router_topk_scatter(lg_t, top_k, renorm, ids, w, st, off, None, None) == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(ids.cpu().numpy(), ids_r)
+        assert np.array_equal(w.cpu().numpy().view(np.uint32), w_r.view(np.uint32))
+
+
 @pytest.mark.parametrize("y_bf16", [True, False])
 def test_gather_is_bit_exact(torch_cuda, y_bf16):
     import exl3c4
