@@ -25,8 +25,8 @@ extern "C" {
 /* Rows of one chunk on the prefill path (six MFMA row tiles share each decoded step). */
 #define EXL3C4_PF_ROWS 96
 /* The prefill plan: PF_PLAN_HDR int32s, then int4 {expert, row0, rows, 0} per chunk. Header: [0] the chunk count;
- * [PF_CUR + 32 (8 g + x)] (g = 0 gate_up, 1 down): XCD x's cursor over the last units of its range in that GEMM,
- * zeroed by the plan, each on its own 128-byte line;
+ * [PF_CUR + 32 (8 g + x)] (g = 0 gate_up, 1 down): XCD x's cursor over the last units of its range in that GEMM
+ * (down deals none by cursor today), zeroed by the plan, each on its own 128-byte line;
  * [PF_SPAN] 1 when the rows the chunks hold are one span, [PF_SPAN + 1] its first row, [PF_SPAN + 2] its end (0: the
  * rows' owners are in row_info instead); [PF_XCD_GU + x], [PF_XCD_DN + x] (x = 0 .. 8): the first chunk of XCD x for
  * gate_up's and down's GEMM ([.. + 8] = the count). A chunk of t 16-row tiles costs about PF_W_GU + t (gate_up) and

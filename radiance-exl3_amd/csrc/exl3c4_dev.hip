@@ -2012,8 +2012,9 @@ __device__ __forceinline__ bool xcd_unit(int per, const int32_t* xb, const int32
     chunk = ord[xb[y] + q];
     return true;
 }
-// each XCD's units dealt by its cursor: about one round of its slots (gate_up: 2 workgroups a CU x 32 CUs; down: 4)
-constexpr int PF_DYN_GU = 64, PF_DYN_DN = 128;
+// each XCD's units dealt by its cursor: gate_up's last round of its slots (2 workgroups a CU x 32 CUs); down's none
+// -- its XCDs end within a few us, and a round dealt by cursors (128 units) measured 2 us slower than static slots
+constexpr int PF_DYN_GU = 64, PF_DYN_DN = 0;
 
 // One k-step of the prefill GEMM: the step's B operands (decoded just before) against each of the chunk's NT row
 // tiles (4 MFMAs a tile), each group ending in mfma_guard: gfx950 does not interlock a VALU or LDS write against an

@@ -222,9 +222,10 @@ def test_prefill_xcd_ranges_hold_every_chunk_of_a_crowded_range(torch_cuda):
 
 def test_prefill_units_dealt_by_the_xcd_cursors(torch_cuda):
     """Two experts of 1,900 and 148 rows (top_k 1, 2,048 sorted rows, 22 chunks): each XCD's range holds a few
-    chunks' units, fewer than the round a cursor deals, so every unit of both GEMMs goes out through the XCDs'
-    cursors, and the XCDs whose ranges are spent (or empty) take units from the others. Every op of the case meets
-    the oracle, the rows of y and h equal to the bit across a replay (each unit handed out once, wherever it ran)."""
+    chunks' units, fewer than the round a cursor deals, so every unit of gate_up's GEMM goes out through the XCDs'
+    cursors, and the XCDs whose ranges are spent (or empty) take units from the others (down's units keep their
+    slots). Every op of the case meets the oracle, and a replay writes the same bits (each unit handed out once,
+    wherever it ran)."""
     import exl3c4
     ids = np.array([0] * 1900 + [1] * 148, dtype=np.int32)
     ids = np.random.default_rng(99).permutation(ids)[:, None]
