@@ -22,8 +22,10 @@ extern "C" {
  * where in a row's line the count of its down units past their wait sits */
 #define EXL3C4_SYNC_STRIDE 64
 #define EXL3C4_SYNC_DONE 32
-/* Rows of one chunk on the prefill path (six MFMA row tiles share each decoded step). */
-#define EXL3C4_PF_ROWS 96
+/* Rows of one chunk on the prefill path at most: seven MFMA row tiles share each decoded step where a launch's K are
+ * at most 4, six (EXL3C4_PF_ROWS_WIDE) at larger K. */
+#define EXL3C4_PF_ROWS 112
+#define EXL3C4_PF_ROWS_WIDE 96
 /* The prefill plan: PF_PLAN_HDR int32s, then int4 {expert, row0, rows, 0} per chunk. Header: [0] the chunk count;
  * [PF_CUR + 32 (8 g + x)] (g = 0 gate_up, 1 down): XCD x's cursor over the last units of its range in that GEMM
  * (down deals none by cursor today), zeroed by the plan, each on its own 128-byte line;

@@ -1210,6 +1210,11 @@ __global__ __launch_bounds__(256) void k_fill(int32_t* p, int64_t n) {
 // ranges of about equal cost (a chunk of t tiles: W + t; its midpoint in cost order picks the XCD); then each row's
 // owner. Its own kernel (k_plan), or the first workgroup of k_rot's launch, running beside the rotation.
 constexpr int PF_TILES = EXL3C4_PF_ROWS / 16;                     // row tiles a chunk holds at most
+// The rows a chunk of this launch holds: seven row tiles where both GEMMs decode at K <= 4 (their loops then hold
+// seven tiles of accumulators in the 128 registers of 4 waves a SIMD), six at larger K (seven would spill there)
+__device__ __forceinline__ int pf_rows(const Exl3c4Launch& a) {
+    return a.bits <= 4 && a.dn_bits <= 4 ? EXL3C4_PF_ROWS : EXL3C4_PF_ROWS_WIDE;
+}
 // The plan's chunk order of one GEMM (gate_up 0, down 1): max_chunks entries after the chunk entries.
 __device__ __forceinline__ const int32_t* pf_order(const Exl3c4Launch& a, int gemm) {
     return a.plan + EXL3C4_PF_PLAN_HDR + 4 * a.max_chunks + gemm * a.max_chunks;
@@ -1231,6 +1236,7 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
     __shared__ int carry_s, tiles_s, cut_s, cnt_g[8], cnt_d[8];
     __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
     const int tid = threadIdx.x;
+    const int R = pf_rows(a);                                      // a chunk's rows at most
     if (tid == 0) {
         carry_s = tiles_s = 0;
         cut_s = 0x7FFFFFFF;
@@ -1245,7 +1251,7 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
         if (e < a.n_expert) {
             lo = min(max(a.off[e], 0), a.T);
             hi = min(max(a.off[e + 1], lo), a.T);
-            n = (hi - lo + EXL3C4_PF_ROWS - 1) / EXL3C4_PF_ROWS;
+            n = (hi - lo + R - 1) / R;
         }
         scan[tid] = n;
         __syncthreads();
@@ -1260,7 +1266,7 @@ template <int NT> __device__ __forceinline__ void plan_generic(const Exl3c4Launc
         for (int q = 0; q < n; ++q) {
             const int at = first + q;
             if (at < a.max_chunks) {
-                const int r0 = lo + q * EXL3C4_PF_ROWS, rows = min(EXL3C4_PF_ROWS, hi - r0);
+                const int r0 = lo + q * R, rows = min(R, hi - r0);
                 ent[at] = make_int4(e, r0, rows, 0);
                 tiles += (rows + 15) >> 4;
             }
@@ -1402,14 +1408,14 @@ template <int NT> __device__ __forceinline__ int64_t block_scan64(int64_t v, int
 // first chunks and tile prefixes kept in LDS, each entry written and read by its own thread): one round of loads (the
 // offsets), then scans, LDS counters and stores only -- nothing the workgroup writes to global memory is read back, so
 // no phase waits for its stores. The same plan as plan_generic: chunks in expert order, each expert's run clamped to
-// [0, T) and cut into chunks of at most EXL3C4_PF_ROWS rows (all full but the last), the chunks past max_chunks
+// [0, T) and cut into chunks of at most pf_rows rows (all full but the last), the chunks past max_chunks
 // dropped (their rows' owner -1); each chunk's XCDs from its cost midpoint; each GEMM's order by tiles inside an
 // XCD's range; the rows' owners.
 // The plan for up to EPT x NT experts, thread tid taking experts tid, NT + tid, ... (their clamped runs, first chunks
 // and tile prefixes kept in LDS, each entry written and read by its own thread): one round of loads (the offsets),
 // then scans, LDS counters and stores only -- nothing the workgroup writes to global memory is read back, so no phase
 // waits for its stores. The same plan as plan_generic: chunks in expert order, each expert's run clamped to [0, T) and
-// cut into chunks of at most EXL3C4_PF_ROWS rows (all full but the last), the chunks past max_chunks dropped; each
+// cut into chunks of at most pf_rows rows (all full but the last), the chunks past max_chunks dropped; each
 // chunk's XCDs from its cost midpoint; each GEMM's order by tiles inside an XCD's range. A thread's chunks of one
 // expert fall into runs of equal (XCD, tiles) -- the XCD grows with the chunk index -- and each run costs one LDS
 // atomic: the counts added when a run ends, a run's slots in the order taken by one atomicAdd of its length. The rows'
@@ -1422,6 +1428,7 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
     __shared__ int cur_g[8][PF_TILES], cur_d[8][PF_TILES];           // per (XCD, tiles): chunk counts, then cursors
     __shared__ int s_lo[EPT * NT], s_hi[EPT * NT], s_first[EPT * NT], s_tf[EPT * NT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int R = pf_rows(a), RT = R >> 4;                         // a chunk's rows and tiles at most
     if (tid < 8) cnt_g[tid] = cnt_d[tid] = 0;
     if (tid == 0) {
         tk_s = desc_s = 0;
@@ -1443,9 +1450,9 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
         const int e = k * NT + tid;
         desc = desc || (e < a.n_expert && hi[k] < lo[k]);
         const int l = min(max(lo[k], 0), a.T), h = min(max(hi[k], l), a.T);
-        const int n = e < a.n_expert ? (h - l + EXL3C4_PF_ROWS - 1) / EXL3C4_PF_ROWS : 0;
-        const int rem = h - l - (n - 1) * EXL3C4_PF_ROWS;        // the last chunk's rows
-        const int tiles = n ? (n - 1) * PF_TILES + ((rem + 15) >> 4) : 0;
+        const int n = e < a.n_expert ? (h - l + R - 1) / R : 0;
+        const int rem = h - l - (n - 1) * R;                      // the last chunk's rows
+        const int tiles = n ? (n - 1) * RT + ((rem + 15) >> 4) : 0;
         const int64_t v = ((int64_t)tiles << 32) | (uint32_t)n;
         int64_t blk;
         const int64_t ex = carry + block_scan64<NT>(v, wsum, blk) - v;
@@ -1466,8 +1473,8 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
             const int e = k * NT + tid;
             if (e >= a.n_expert) break;
             const int l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
-            for (int r0 = l, at = f, p = tf; r0 < h; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES)
-                if (p + ((min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4) > budget) {
+            for (int r0 = l, at = f, p = tf; r0 < h; r0 += R, ++at, p += RT)
+                if (p + ((min(R, h - r0) + 15) >> 4) > budget) {
                     atomicMin(&cut_s, at);
                     break;
                 }
@@ -1482,8 +1489,8 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
 #pragma unroll 1
         for (int k = 0; k < EPT; ++k) {
             const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e];
-            for (int r0 = l, at = f; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at)
-                t += (min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4;
+            for (int r0 = l, at = f; r0 < h && at < nch; r0 += R, ++at)
+                t += (min(R, h - r0) + 15) >> 4;
         }
         if (t) atomicAdd(&tk_s, t);
         __syncthreads();
@@ -1498,8 +1505,8 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
         if (k * NT >= a.n_expert) break;                          // uniform
         const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
         int kg = -1, kd = -1, ng = 0, nd = 0;
-        for (int r0 = l, at = f, p = tf; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES) {
-            const int rows = min(EXL3C4_PF_ROWS, h - r0), t = (rows + 15) >> 4;   // earlier chunks: full
+        for (int r0 = l, at = f, p = tf; r0 < h && at < nch; r0 += R, ++at, p += RT) {
+            const int rows = min(R, h - r0), t = (rows + 15) >> 4;   // earlier chunks: full
             const int xg = pf_xcd_of(EXL3C4_PF_W_GU * at + p, EXL3C4_PF_W_GU + t, tot_g);
             const int xd = pf_xcd_of(EXL3C4_PF_W_DN * at + p, EXL3C4_PF_W_DN + t, tot_d);
             ent[at] = make_int4(e, r0, rows, xg | (xd << 8));
@@ -1576,8 +1583,8 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
         if (k * NT >= a.n_expert) break;                          // uniform
         const int e = k * NT + tid, l = s_lo[e], h = s_hi[e], f = s_first[e], tf = s_tf[e];
         int kg = -1, kd = -1, ng = 0, nd = 0, at = f;
-        for (int r0 = l, p = tf; r0 < h && at < nch; r0 += EXL3C4_PF_ROWS, ++at, p += PF_TILES) {
-            const int t = (min(EXL3C4_PF_ROWS, h - r0) + 15) >> 4;
+        for (int r0 = l, p = tf; r0 < h && at < nch; r0 += R, ++at, p += RT) {
+            const int t = (min(R, h - r0) + 15) >> 4;
             const int cg = pf_xcd_of(EXL3C4_PF_W_GU * at + p, EXL3C4_PF_W_GU + t, tot_g) * PF_TILES + t - 1;
             const int cd = pf_xcd_of(EXL3C4_PF_W_DN * at + p, EXL3C4_PF_W_DN + t, tot_d) * PF_TILES + t - 1;
             if (cg != kg) {
@@ -1608,7 +1615,7 @@ template <int NT, int EPT> __device__ __forceinline__ void plan_fast(const Exl3c
         const int e0 = k * NT + 64 * wave;
         if (e0 >= a.n_expert) break;                              // uniform
         const int ml = s_lo[e0 + lane];                           // the wave's 64 experts, lane-parallel
-        const int mh = min(s_hi[e0 + lane], ml + max(0, nch - s_first[e0 + lane]) * EXL3C4_PF_ROWS);   // past it:
+        const int mh = min(s_hi[e0 + lane], ml + max(0, nch - s_first[e0 + lane]) * R);   // past it:
         for (int j = 0; j < 64; ++j) {                                                                // dropped
             const int l = __builtin_amdgcn_readlane(ml, j), hk = __builtin_amdgcn_readlane(mh, j);   // chunks' rows,
             for (int r = l + lane; r < hk; r += 64) a.row_info[2 * r] = e0 + j;                      // left -1
@@ -2023,6 +2030,8 @@ constexpr int PF_DYN_GU = 64, PF_DYN_DN = 0;
 // find no slot beside it; a step issued behind the next step's decode, or the waves split into a decoding and a
 // multiplying half each half-step, gained nothing.)
 constexpr int PF_NT = EXL3C4_PF_ROWS / 16;                      // a chunk's row tiles at most
+// a chunk's row tiles at most at K = BITS (pf_rows: seven where the launch's K are at most 4)
+template <int BITS> constexpr int pf_nt() { return BITS <= 4 ? EXL3C4_PF_ROWS / 16 : EXL3C4_PF_ROWS_WIDE / 16; }
 template <int BITS, int CB, int NT>
 __device__ __forceinline__ void pf_step(const uint16_t* Ab, int kp, const uint32_t (&B)[16], float4_t (&acc)[PF_NT][2]) {
     // the segment's B[j] holds the k pair 2 j' of the lane's 16-group for j' = (0, 4, 1, 5, 2, 6, 3, 7)[j & 7] (the
@@ -2100,8 +2109,15 @@ __device__ __forceinline__ void pf_gemm(const void* codes, int32_t codes_s, int 
                                         const uint16_t* src, int64_t pitch, int row0, int nrows, int col_off,
                                         int half_off, uint16_t* lds, float4_t (&acc)[PF_NT][2]) {
 #define EXL3C4_PF_ARGS codes, codes_s, KC, jx, strip, src, pitch, row0, nrows, col_off, half_off, lds, acc
-    static_assert(PF_NT == 6, "pf_gemm instantiates 1 to 6 row tiles");
-    switch ((nrows + 15) >> 4) {
+    static_assert(PF_NT == 7, "pf_gemm instantiates 1 to 7 row tiles");
+    const int nt = (nrows + 15) >> 4;                             // at most pf_nt<BITS>: the plan's pf_rows
+    if constexpr (pf_nt<BITS>() == 7) {
+        if (nt >= 7) {
+            pf_gemm_nt<BITS, CB, NH, 7>(EXL3C4_PF_ARGS);
+            return;
+        }
+    }
+    switch (nt) {
     case 1: pf_gemm_nt<BITS, CB, NH, 1>(EXL3C4_PF_ARGS); break;
     case 2: pf_gemm_nt<BITS, CB, NH, 2>(EXL3C4_PF_ARGS); break;
     case 3: pf_gemm_nt<BITS, CB, NH, 3>(EXL3C4_PF_ARGS); break;
@@ -2186,7 +2202,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const bool yw = ((((uintptr_t)a.y) | ((uintptr_t)a.y_pitch * 2)) & 15) == 0;
     float* acc_l = (float*)lds;                                   // [48][ACC_PITCH], over the staging buffers
 #pragma unroll
-    for (int p = 0; p < PF_NT / EPI_T; ++p) {
+    for (int p = 0; p < (pf_nt<BITS>() + EPI_T - 1) / EPI_T; ++p) {   // the last pass may hold fewer tiles
         const int r0 = p * EPI_T * 16;                            // the pass's first chunk row
         if (r0 >= nrows) break;                                   // uniform
         if (p) __syncthreads();                                   // the previous pass's rows are read
@@ -2195,7 +2211,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int t = p * EPI_T + tt, row = t * 16 + rg * 4 + q;
-                if (row < nrows) {
+                if (t < pf_nt<BITS>() && row < nrows) {
                     if (a.keep_sums) {
                         a.part[(int64_t)(row0 + row) * a.part_pitch + n] = acc[t][0][q];
                         a.part[(int64_t)(row0 + row) * a.part_pitch + n + 8] = acc[t][1][q];
@@ -2284,11 +2300,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
         return;
     }
-    // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane
-    const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
     float4_t acc[PF_NT][2];                                       // pf_gemm zeroes the chunk's tiles
     pf_gemm<BITS, CB, 1>(D.codes, D.codes_s, D.cols, jx, 4 * b + wave, (const uint16_t*)a.x, a.x_pitch, row0, nrows, 0, 0,
                          lds, acc);
+    // the chunk's sorted_tok, lane q holding row q (srt) and row 64 + q (srt2), taken by readlane: loaded after the
+    // GEMM, so that at K <= 4 the loop's seven row tiles of accumulators fit 4 waves a SIMD without a spill
+    const int srt = a.sorted[row0 + min(lane, nrows - 1)], srt2 = a.sorted[row0 + min(64 + lane, nrows - 1)];
 
     // The epilogue, a tile's 16 rows at a time: the sums cross LDS, then wave w takes the tile's rows 4 w .. 4 w + 3,
     // a 16-lane row of the wave per row, lane l holding the 8 consecutive columns 8 g .. 8 g + 7 of the block
@@ -2315,7 +2332,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int ntile = (nrows + 15) >> 4;
     const int lrow = 4 * wave + (lane >> 4);                      // this lane's row of a tile
 #pragma unroll
-    for (int t = 0; t < PF_NT; ++t) {                             // unrolled: acc[t] stays in registers
+    for (int t = 0; t < pf_nt<BITS>(); ++t) {                     // unrolled: acc[t] stays in registers
         if (t >= ntile) break;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {

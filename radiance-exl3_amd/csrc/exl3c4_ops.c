@@ -152,7 +152,7 @@ static void carve(const Exl3c4Op* o, int64_t T, Carve* k) {
     if (gu || (dn && k->pf)) off += ALIGN_UP(T * 8, 256);
     k->plan = off;
     if (k->pf) {
-        k->max_chunks = T / EXL3C4_PF_ROWS + (o->n_expert < T ? o->n_expert : T) + 1;
+        k->max_chunks = T / EXL3C4_PF_ROWS_WIDE + (o->n_expert < T ? o->n_expert : T) + 1;   /* the smaller chunks */
         off += ALIGN_UP(4 * EXL3C4_PF_PLAN_HDR + 24 * k->max_chunks, 256);   /* entries, then two chunk orders */
     }
     k->xr = off;
