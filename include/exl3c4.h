@@ -172,10 +172,11 @@ int     exl3c4_launch_noalloc(const Exl3c4Op* op, void* stream);
 enum { EXL3C4_K_PREP = 0, EXL3C4_K_GATE_UP = 1, EXL3C4_K_EPI_GU = 2, EXL3C4_K_DOWN = 3, EXL3C4_K_GATE_UP_DOWN = 4 };
 #define EXL3C4_GD_FUSE_MIN_T 32
 
-/* The least sorted-row count T at which gate_up, down and gate_up_down over n_expert experts take the prefill path (a chunk plan and one GEMM kernel a projection, decoding each weight once a chunk of up to 96
- * rows of one expert) rather than the decode kernels: max(64, ceil(3 n_expert / 4)) -- the crossover measured on
- * MI355X at the decode layer's experts. A function of T and n_expert only, never of the routing. A query with no
- * counterpart in the reference (whose rows split the band at M = 17, kernels/exl3r4d/rows.c:255-315). */
+/* The least sorted-row count T at which gate_up, down and gate_up_down over n_expert experts take the prefill path (a
+ * chunk plan and one GEMM kernel a projection, decoding each weight once a chunk of up to 112 rows of one expert, 96
+ * where the launch's K exceed 4) rather than the decode kernels: max(64, ceil(7 n_expert / 8)) -- the crossover
+ * measured on MI355X at the decode layer's experts. A function of T and n_expert only, never of the routing. A query
+ * with no counterpart in the reference (whose rows split the band at M = 17, kernels/exl3r4d/rows.c:255-315). */
 int64_t exl3c4_prefill_min_rows(int64_t n_expert);
 
 /* exl3c4_launch, with kernel `kernel` of the sequence dispatched so that the dispatch itself stamps ev_start and

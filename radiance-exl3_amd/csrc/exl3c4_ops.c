@@ -79,24 +79,25 @@ static int log2i(int v) {
     return l;
 }
 
-/* The prefill path (the rotation with the chunk plan, then one GEMM kernel a projection over chunks of up to 96 rows of
- * one expert) serves a launch of at least 64 sorted rows that average at least 3/4 of a row an expert: T >= 64 and
- * 4 T >= 3 n_expert (exl3c4_prefill_min_rows). Below it the decode kernels serve it (chunks of up to 16 rows, split-K;
+/* The prefill path (the rotation with the chunk plan, then one GEMM kernel a projection over chunks of up to 112 rows
+ * of one expert) serves a launch of at least 64 sorted rows that average at least 7/8 of a row an expert: T >= 64 and
+ * 8 T >= 7 n_expert (exl3c4_prefill_min_rows). Below it the decode kernels serve it (chunks of up to 16 rows, split-K;
  * gate_up_down as one kernel from EXL3C4_GD_FUSE_MIN_T rows). The rule is the crossover measured on MI355X at the
  * decode layer's experts (512 experts, 2048 / 512, K = 4, softmax top-10): gate_up_down by the decode kernels against
- * the prefill kernels, us a launch, M tokens: M = 17: 82 / 99, 24: 108 / 117, 32: 135 / 135, 40: 153 / 155,
- * 48: 172 / 163, 64: 204 / 191 (and, measured on an earlier build, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293):
- * the rule's M >= 39 (T >= 384) sits in the band where the two differ by under 2%. The reference serves M >= 17 by
- * its GEMM rows (kernels/exl3r4d/rows.c:255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the
- * band below the crossover. A function of T, n_expert and the op's widths (never of the routing): the prefill GEMMs address a chunk's
- * staged rows by 32-bit byte offsets (2 x 95 x pitch + 64 < 2^32), so an input pitch past EXL3C4_PF_MAX_PITCH halves
- * (the caller's x, the rotated input's 2 x cols, h's rows / 2) keeps the decode kernels at any T. */
+ * the prefill kernels, us a launch, M tokens (3 x 400 launches, alternating on one box): M = 26: 107.7 / 126.4,
+ * 28: 113.9 / 128.2, 32: 127.6 / 131.0, 36: 139.6 / 152.0, 40: 151.5 / 156.5, 44: 155.5 / 157.8, 48: 169.1 / 160.8,
+ * 56: 186.8 / 186.0 (an earlier build: 64: 204 / 191, 128: 302 / 264, 256: 389 / 285, 409: 491 / 293): the rule's
+ * M >= 45 (T >= 448) sits between 44 and 48. The reference serves M >= 17 by its GEMM rows (kernels/exl3r4d/rows.c:
+ * 255-315, kernels/exl3r4d/prefill.c:61-76); here the decode kernels keep the band below the crossover. A function of
+ * T, n_expert and the op's widths (never of the routing): the prefill GEMMs address a chunk's staged rows by 32-bit
+ * byte offsets (2 x 111 x pitch + 64 < 2^32), so an input pitch past EXL3C4_PF_MAX_PITCH halves (the caller's x, the
+ * rotated input's 2 x cols, h's rows / 2) keeps the decode kernels at any T. */
 #ifndef EXL3C4_PF_MIN_T
 #define EXL3C4_PF_MIN_T 64
 #endif
 #define EXL3C4_PF_MAX_PITCH (1 << 24)
 int64_t exl3c4_prefill_min_rows(int64_t n_expert) {
-    const int64_t r = (3 * (n_expert > 0 ? n_expert : 0) + 3) / 4;
+    const int64_t r = (7 * (n_expert > 0 ? n_expert : 0) + 7) / 8;
     return r > EXL3C4_PF_MIN_T ? r : EXL3C4_PF_MIN_T;
 }
 static int prefill_path(const Exl3c4Op* o, int64_t T) {

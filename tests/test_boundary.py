@@ -61,7 +61,7 @@ BANDS = [
     (exl3c4.GATE_UP, 2048, 512, 512, 16, 10),    # the decode band top M = 16
     (exl3c4.DOWN, 2048, 512, 512, 16, 10),
     (exl3c4.GU_DN, 2560, 640, 512, 16, 10),      # the reference's per-rank geometry
-    (exl3c4.GU_DN, 2048, 512, 512, 96, 10),      # a band across the prefill threshold (384 rows here)
+    (exl3c4.GU_DN, 2048, 512, 512, 96, 10),      # a band across the prefill threshold (448 rows here)
 ]
 
 

@@ -160,10 +160,10 @@ def test_prefill_path_four_classes_mcg(torch_cuda):
 def test_owner_search_on_both_sides_of_its_one_round_form(torch_cuda, n_expert):
     """The rotation kernels' owner search (k_prep's and k_rot's) holds the run offsets of up to 575 experts in one round
     of loads and reads the owner's run bounds out of its registers; from 576 experts it loops over the offsets and
-    loads the bounds again. 480 sorted rows over 575, 576 and 600 experts (the prefill path: T >= 3/4 n_expert), with
+    loads the bounds again. 600 sorted rows over 575, 576 and 600 experts (the prefill path: T >= 7/8 n_expert), with
     dropped slots, through every op against the oracle."""
     import exl3c4
-    case = Case(seed=45 + n_expert, n_tok=120, top_k=4, n_expert=n_expert, geoms=[(256, 128)], bits=4, cb="mul1",
+    case = Case(seed=45 + n_expert, n_tok=150, top_k=4, n_expert=n_expert, geoms=[(256, 128)], bits=4, cb="mul1",
                 drop=0.05)
     assert exl3c4.is_prefill(case.T, case.n_expert)
     _check_all(case, f"owner search, {n_expert} experts")
@@ -195,10 +195,10 @@ def test_prefill_plan_with_offsets_that_do_not_ascend(torch_cuda):
 
 def test_prefill_plan_past_its_register_form(torch_cuda):
     """1040 experts: past the 4 x 256 experts the rotation launch's planning workgroup holds in its threads, so the
-    plan takes its general form (blocks of 256 experts, the entries read back); 800 sorted rows, every op against
+    plan takes its general form (blocks of 256 experts, the entries read back); 960 sorted rows, every op against
     the oracle."""
     import exl3c4
-    case = Case(seed=93, n_tok=200, top_k=4, n_expert=1040, geoms=[(256, 128)], bits=4, cb="mul1", drop=0.05)
+    case = Case(seed=93, n_tok=240, top_k=4, n_expert=1040, geoms=[(256, 128)], bits=4, cb="mul1", drop=0.05)
     assert exl3c4.is_prefill(case.T, case.n_expert)
     _check_all(case, "prefill 1040 experts")
 
