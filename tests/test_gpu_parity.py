@@ -138,16 +138,43 @@ def test_gate_up_down_as_one_kernel_at_the_layer_geometry(torch_cuda):
 
 
 # ------------------------------------------------------------------------------------------ the prefill path
-# (from exl3c4_prefill_min_rows(n_expert) sorted rows: chunks of up to 96 rows, a plan, the rotation into scratch, the
-# prefill GEMMs)
+# (from exl3c4_prefill_min_rows(n_expert) sorted rows: chunks of up to 112 rows where the launch's K are at most 4, 96
+# above, a plan, the rotation into scratch, the prefill GEMMs)
 def test_prefill_path_two_classes_several_chunks_with_drops(torch_cuda):
-    """Runs of 126, 53, 111 and 63 rows: two experts cut into a full 96-row chunk (six row tiles, rows past 64 read
-    their sorted_tok from the second register) and a short one, the others one chunk of 4 tiles."""
+    """Runs of 126, 53, 111 and 63 rows at K = 4 (chunks of up to 112 rows): 126 cut into a full chunk of seven row
+    tiles (rows past 64 read their sorted_tok from the second register) and a short one, 111 one chunk of seven
+    tiles, the others one chunk of four."""
     case = Case(seed=40, n_tok=200, top_k=2, n_expert=4, geoms=[(256, 256), (384, 128)], bits=4, cb="mul1",
                 drop=0.1, protect_tail=2, routing="zipf")
     import exl3c4
     assert exl3c4.is_prefill(case.T, case.n_expert) and np.diff(case.off).max() > 96
     _check_all(case, "prefill two-class")
+
+
+@pytest.mark.parametrize("bits,dn_bits", [(4, 4), (6, 6), (4, 6)])
+def test_prefill_chunks_by_k(torch_cuda, bits, dn_bits):
+    """A run of 250 rows beside one of 50 (top_k 1, 300 sorted rows): at K 4 / 4 the plan cuts it into chunks of 112
+    rows (seven row tiles), at 6 / 6 and at gate_up 4 with down 6 (one launch, down's K apart) into chunks of 96 (six:
+    the kernels at K > 4 hold no seventh tile); every op of the case against the oracle."""
+    import exl3c4
+    ids = np.random.default_rng(96).permutation(np.array([0] * 250 + [1] * 50, dtype=np.int32))[:, None]
+    case = Case(seed=96, n_tok=300, top_k=1, n_expert=2, geoms=[(256, 128)], bits=bits, cb="mul1", expert_ids=ids,
+                dn_bits=dn_bits)
+    assert case.T == 300 and exl3c4.is_prefill(case.T, case.n_expert)
+    if bits == dn_bits:
+        _check_all(case, f"prefill chunks K {bits}")
+        return
+    from gpuchecks import chain_ok
+    _say(f"prefill chunks K {bits} / {dn_bits}")                # one launch of mixed K: its split chain's bits
+    dev = Dev(case)
+    gd = dev.gate_up_down()
+    h1 = dev.gate_up(h_rot=1)
+    h1_o = case.oracle_gate_up(h_rot=1)
+    assert chain_ok("gate_up h_rot 1", f16(h1), f16(h1_o))
+    assert np.array_equal(dev.down(h1, h_rot=1), gd)
+    assert narrowed_ok(gd, case.oracle_down(h1, h_rot=1), "bf16") == 0
+    assert chain_ok("mixed chain", bf16(gd), bf16(case.oracle_down(h1_o, h_rot=1)))
+    dev.check_tables()
 
 
 def test_prefill_path_four_classes_mcg(torch_cuda):
